@@ -1,0 +1,299 @@
+"""Benchmark of the Seera GEMM / conv hot path on one MI355X.
+
+Headline (BASELINE.json metric "GEMM TFLOP/s (% MFMA peak) at 4096^3 fp16;
+Conv2D fwd+bwd TFLOP/s"): one step = one C = A.B GEMM at M = N = K = 4096
+(A, B ~ U[-1,1] rounded to fp16, seed 4096) through the C
+ABI, inputs resident in HBM. Timed with HIP events on the stream the kernels
+run on, W untimed warm-up steps, then exactly K timed steps with a device
+synchronize on both sides.
+
+Also reported (same run, fewer repetitions): GEMM fwd+bwd at 4096^3, Conv2D
+3x3 fwd+bwd (config 4), ConvTranspose2D 4x4 s2 fwd+bwd (config 5), the
+MLP 784-512-256-10 GEMMs (config 3), and the CPU baseline (the oracle's
+restatement of seera_cpp on OpenBLAS, on this host's cores).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from ml_framework_amd import capi  # noqa: E402
+from ml_framework_amd.capi import DeviceBuffer, Event  # noqa: E402
+
+METRIC = "GEMM TFLOP/s (% MFMA peak) at 4096³ fp16; Conv2D fwd+bwd TFLOP/s"
+PEAK_FP16_TFLOPS = 2516.6   # MI355X dense fp16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+PEAK_HBM_GBS = 8000.0
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def fp16r(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+class Stream:
+    def __init__(self):
+        import ctypes
+
+        p = ctypes.c_void_p()
+        capi.check(capi.load().seera_hip_stream_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def sync(self):
+        capi.check(capi.load().seera_hip_stream_synchronize(self.ptr))
+
+
+def timed(fn, steps, warmup, stream):
+    """Run fn() warmup times, then time exactly `steps` calls with events on
+    `stream`, bracketed by device synchronizes. Returns ms per call."""
+    for _ in range(warmup):
+        fn()
+    capi.check(capi.load().seera_hip_synchronize())
+    t0, t1 = Event(), Event()
+    t0.record(stream.ptr)
+    for _ in range(steps):
+        fn()
+    t1.record(stream.ptr)
+    capi.check(capi.load().seera_hip_synchronize())
+    return t0.elapsed_ms(t1) / steps
+
+
+def bench_gemm(n, steps, warmup, stream, with_bwd):
+    r = np.random.default_rng(n)
+    a = fp16r(r.uniform(-1, 1, (n, n)))
+    b = fp16r(r.uniform(-1, 1, (n, n)))
+    dc = fp16r(r.uniform(-1, 1, (n, n)))
+    lib = capi.load()
+    bufs = [DeviceBuffer.from_array(x) for x in (a, b, dc)]
+    pa, pb, pdc = (x.ptr for x in bufs)
+    outs = [DeviceBuffer(n * n * 4) for _ in range(3)]
+    pc, pda, pdb = (x.ptr for x in outs)
+
+    def fwd():
+        capi.check(lib.seera_hip_matmul_async(pa, pb, pc, n, n, n, 1, stream.ptr))
+
+    def fwdbwd():
+        fwd()
+        capi.check(lib.seera_hip_matmul_bwd_async(pa, pb, pdc, pda, pdb, n, n, n, 1, stream.ptr))
+
+    ms = timed(fwd, steps, warmup, stream)
+    res = {"ms_fwd": ms}
+    # light parity check of the timed output: 16 rows against fp64
+    rows = np.arange(0, n, n // 16)
+    c = outs[0].to_array((n, n))
+    ref = a[rows].astype(np.float64) @ b
+    res["rel_fro_sampled"] = float(np.linalg.norm(c[rows] - ref) / np.linalg.norm(ref))
+    if with_bwd:
+        res["ms_fwd_bwd"] = timed(fwdbwd, max(steps // 4, 5), 2, stream)
+    for x in bufs + outs:
+        x.close()
+    return res
+
+
+def bench_conv(steps, warmup, stream):
+    """Config 4: Conv2D 3x3 s1 p1, N=128, 64->64, 56x56; fwd + (dX, dW)."""
+    r = np.random.default_rng(0)
+    N, C, H, W, F = 128, 64, 56, 56, 64
+    x = fp16r(r.standard_normal((N, C, H, W)))
+    lim = np.sqrt(6 / 576)
+    w = fp16r(r.uniform(-lim, lim, (F, C, 3, 3)))
+    dy = fp16r(r.standard_normal((N, F, H, W)))
+    lib = capi.load()
+    px, pw, pdy = (DeviceBuffer.from_array(v) for v in (x, w, dy))
+    py, pdx, pdw = DeviceBuffer(x.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(w.nbytes)
+
+    def fwd():
+        capi.check(lib.seera_hip_conv2d_fwd_async(px.ptr, pw.ptr, py.ptr, N, C, H, W, F, 3, 3,
+                                                  1, 1, 1, 1, stream.ptr))
+
+    def bwd():
+        capi.check(lib.seera_hip_conv2d_bwd_async(pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr, N, C,
+                                                  H, W, F, 3, 3, 1, 1, 1, 1, stream.ptr))
+
+    res = {"ms_fwd": timed(fwd, steps, warmup, stream), "ms_bwd": timed(bwd, steps, warmup, stream)}
+    for v in (px, pw, pdy, py, pdx, pdw):
+        v.close()
+    return res
+
+
+def bench_convT(steps, warmup, stream):
+    """Config 5: ConvTranspose2D 4x4 s2 p1, N=32, 128->64, 28x28 -> 56x56."""
+    r = np.random.default_rng(0)
+    N, Cin, H, W, Cout = 32, 128, 28, 28, 64
+    x = fp16r(r.standard_normal((N, Cin, H, W)))
+    lim = np.sqrt(6 / 2048)
+    w = fp16r(r.uniform(-lim, lim, (Cin, Cout, 4, 4)))
+    dy = fp16r(r.standard_normal((N, Cout, 56, 56)))
+    lib = capi.load()
+    px, pw, pdy = (DeviceBuffer.from_array(v) for v in (x, w, dy))
+    py, pdx, pdw = DeviceBuffer(dy.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(w.nbytes)
+
+    def fwd():
+        capi.check(lib.seera_hip_conv2DTranpose_fwd_async(px.ptr, pw.ptr, py.ptr, N, Cin, H, W,
+                                                          Cout, 4, 4, 2, 2, 1, 1, stream.ptr))
+
+    def bwd():
+        capi.check(lib.seera_hip_conv2DTranspose_bwd_async(pw.ptr, px.ptr, pdy.ptr, pdx.ptr,
+                                                           pdw.ptr, N, Cin, H, W, Cout, 4, 4, 2,
+                                                           2, 1, 1, stream.ptr))
+
+    res = {"ms_fwd": timed(fwd, steps, warmup, stream), "ms_bwd": timed(bwd, steps, warmup, stream)}
+    for v in (px, pw, pdy, py, pdx, pdw):
+        v.close()
+    return res
+
+
+def bench_mlp(steps, warmup, stream):
+    """Config 3: the nine GEMMs of MLP 784-512-256-10 fwd+bwd at batch 256."""
+    r = np.random.default_rng(0)
+    dims = [784, 512, 256, 10]
+    lib = capi.load()
+    acts = [DeviceBuffer.from_array(fp16r(r.uniform(0, 1, (256, d)))) for d in dims]
+    ws = [DeviceBuffer.from_array(fp16r(r.uniform(-0.05, 0.05, (i, o))))
+          for i, o in zip(dims[:-1], dims[1:])]
+    grads = [DeviceBuffer(256 * d * 4) for d in dims]
+    dws = [DeviceBuffer(i * o * 4) for i, o in zip(dims[:-1], dims[1:])]
+
+    def step():
+        for li in range(3):
+            capi.check(lib.seera_hip_matmul_async(acts[li].ptr, ws[li].ptr, acts[li + 1].ptr, 256,
+                                                  dims[li + 1], dims[li], 1, stream.ptr))
+        for li in (2, 1, 0):
+            capi.check(lib.seera_hip_matmul_bwd_async(acts[li].ptr, ws[li].ptr,
+                                                      grads[li + 1].ptr, grads[li].ptr,
+                                                      dws[li].ptr, 256, dims[li + 1], dims[li], 1,
+                                                      stream.ptr))
+
+    grads[3].fill(0)
+    ms = timed(step, steps, warmup, stream)
+    for v in acts + ws + grads + dws:
+        v.close()
+    flops = sum(2 * 256 * i * o * 3 for i, o in zip(dims[:-1], dims[1:]))
+    return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+
+
+def cpu_baseline(n=4096, reps=5):
+    """The oracle's seera_cpp restatement (OpenBLAS sgemm) on this host."""
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    oracle.load(threads)
+    r = np.random.default_rng(n)
+    a = fp16r(r.uniform(-1, 1, (n, n)))
+    b = fp16r(r.uniform(-1, 1, (n, n)))
+    S = oracle.seera_cpp
+    S.matmul(a, b)
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        S.matmul(a, b)
+        ts.append(time.perf_counter() - t)
+    sec = float(np.median(ts))
+    return {
+        "value": round(2 * n ** 3 / sec / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n}^3 fp32 GEMM (oracle_matmul over {oracle.backend()}), "
+                  f"median of {reps} after 1 warm-up",
+    }
+
+
+def traffic_from_profiles():
+    """HBM bytes per GEMM launch measured with rocprofv3 --pmc (committed
+    summary under profiles/), or None if not measured."""
+    path = os.path.join(PROFILES, "gemm_fwd_4096_traffic.json")
+    if os.path.exists(path):
+        try:
+            return json.load(open(path)).get("bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU "
+              "(the GEMM/conv hot path is single-device; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not capi.gpu_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    stream = Stream()
+    n = 4096
+    flops = 2.0 * n ** 3
+    g = bench_gemm(n, args.steps, args.warmup, stream, with_bwd=not args.no_extras)
+    ms = g["ms_fwd"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "gemm_fwd_4096", "M": n, "N": n, "K": n,
+                   "operands": "fp32 in HBM, fp16 RNE into MFMA, fp32 accumulate/out",
+                   "seed": n, "parallelism": "single GPU"},
+        "pct_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic_from_profiles(),
+            "kernel": "igemm_kernel<256,256,32,2,2> (GEMM fwd)",
+            "algorithmic": "2*4096^3 FLOP per launch, one launch per step",
+        },
+        "parity": {"gemm_rel_fro_sampled": g["rel_fro_sampled"]},
+    }
+    if not args.no_extras:
+        extras = {"gemm_fwd_bwd_4096_tflops": round(3 * flops / (g["ms_fwd_bwd"] * 1e-3) / 1e12, 2)}
+        cv = bench_conv(20, 3, stream)
+        conv_flops = 29.6e9 * 3  # 2*N*F*Ho*Wo*C*R*S per pass, 3 passes
+        extras["conv2d_cfg4"] = {
+            "ms_fwd": round(cv["ms_fwd"], 4), "ms_bwd": round(cv["ms_bwd"], 4),
+            "fwd_bwd_tflops": round(conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3) / 1e12, 2),
+            "pct_mfma_peak": round(100 * conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3)
+                                   / 1e12 / PEAK_FP16_TFLOPS, 2),
+        }
+        ct = bench_convT(20, 3, stream)
+        ct_flops = 6.58e9 * 3
+        extras["convT_cfg5"] = {
+            "ms_fwd": round(ct["ms_fwd"], 4), "ms_bwd": round(ct["ms_bwd"], 4),
+            "fwd_bwd_tflops": round(ct_flops / ((ct["ms_fwd"] + ct["ms_bwd"]) * 1e-3) / 1e12, 2),
+        }
+        extras["mlp_cfg3"] = {k: round(v, 4) for k, v in bench_mlp(20, 3, stream).items()}
+        out["extras"] = extras
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(n)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

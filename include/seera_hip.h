@@ -1,0 +1,158 @@
+/*
+ * seera_hip.h -- C ABI of the MI355X (gfx950) Seera matmul/conv hot path.
+ *
+ * Every entry point takes plain device pointers (fp32, row-major / NCHW, as
+ * the reference's cuTen buffers hold them) and C ints, and returns a status
+ * code (0 = success). On failure, seera_hip_last_error() gives a message for
+ * the calling thread. Operands are rounded to fp16 (round-to-nearest-even) on
+ * their way into the matrix cores and accumulated in fp32; outputs are fp32
+ * and are overwritten, never accumulated into.
+ *
+ * The plain entry points keep the reference's "result ready on return"
+ * contract (they synchronize the device before returning, like every wrapper
+ * in engine_cuda/src). The *_async forms enqueue on `stream` (a hipStream_t;
+ * NULL = the null stream) and return without synchronizing.
+ */
+#ifndef SEERA_HIP_H
+#define SEERA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SEERA_OK = 0,
+    SEERA_ERR_INVALID_ARGUMENT = 1, /* bad dims, null pointer, int overflow */
+    SEERA_ERR_HIP = 2,              /* a HIP runtime call or launch failed */
+    SEERA_ERR_OUT_OF_MEMORY = 3,    /* device allocation failed */
+};
+
+/* Message describing the last failure on this thread ("" if none). */
+const char *seera_hip_last_error(void);
+/* Library version string. */
+const char *seera_hip_version(void);
+/* Number of visible devices, or -1 when no HIP device is present. */
+int seera_hip_device_count(void);
+
+/* ---- memory and transfer: engine_cuda/src/cuda_bindings.cpp:23-170 ---- */
+
+/* cuda_malloc / cuda_malloc_f32 / _i32 / _i16 / _f16 (cuda_bindings.cpp:23-56). */
+int seera_hip_malloc(void **out, size_t nbytes);
+/* cuda_free (cuda_bindings.cpp:58-59). NULL is a no-op. */
+int seera_hip_free(void *ptr);
+/* cuda_memset (cuda_bindings.cpp:65-66). */
+int seera_hip_memset(void *ptr, int value, size_t nbytes);
+/* cuda_memcopy_devicetodevice (cuda_bindings.cpp:61-62): dst <- src. */
+int seera_hip_memcpy_d2d(void *dst, const void *src, size_t nbytes);
+/* to_device_* (cuda_bindings.cpp:73-80, 98-105, 155-170): host -> device. */
+int seera_hip_memcpy_h2d(void *dst, const void *src, size_t nbytes);
+/* to_host_* (cuda_bindings.cpp:82-96, 107-153): device -> host. */
+int seera_hip_memcpy_d2h(void *dst, const void *src, size_t nbytes);
+/* cudaDeviceSynchronize as closed every reference wrapper. */
+int seera_hip_synchronize(void);
+
+/* ---- GEMM: engine_cuda/src/GEMM.cu ---- */
+
+/* cuda_matmul (GEMM.cu:95-103; binding cuda_bindings.cpp:260-264).
+ * C[b] = A[b] . B for b < Nbatch: A [Nbatch,M,K], B [K,N] (shared across the
+ * batch), C [Nbatch,M,N]. */
+int seera_hip_matmul(const float *A, const float *B, float *C, int M, int N,
+                     int K, int Nbatch);
+int seera_hip_matmul_async(const float *A, const float *B, float *C, int M,
+                           int N, int K, int Nbatch, void *stream);
+
+/* cuda_matmul_bwd (GEMM.cu:164-225; binding cuda_bindings.cpp:267-273).
+ * dA[b] = dC[b] . B^T  and  dB = sum_b A[b]^T . dC[b]; both overwritten. */
+int seera_hip_matmul_bwd(const float *A, const float *B, const float *dC,
+                         float *dA, float *dB, int M, int N, int K,
+                         int Nbatch);
+int seera_hip_matmul_bwd_async(const float *A, const float *B, const float *dC,
+                               float *dA, float *dB, int M, int N, int K,
+                               int Nbatch, void *stream);
+
+/* cuda_transpose_2d (GEMM.cu:229-235; binding cuda_bindings.cpp:276-280).
+ * out[c,r] = in[r,c], bit-exact. */
+int seera_hip_transpose_2d(const float *in, float *out, int rows, int cols);
+
+/* cuda_transpose_3d (GEMM.cu:143-150; binding cuda_bindings.cpp:283-287).
+ * out[b,k,m] = in[b,m,k], bit-exact. */
+int seera_hip_transpose_3d(const float *in, float *out, int Nbatch, int M,
+                           int K);
+
+/* ---- Conv2D: engine_cuda/src/convolution.cu ---- */
+
+/* cuda_conv2d_fwd (convolution.cu:367-389; binding cuda_bindings.cpp:294-299).
+ * NOTE the argument order: pad before stride.
+ * conv[b,n,ho,wo] = sum_{c,r,s} kernel[n,c,r,s] *
+ *                   image[b,c,ho*stride_h-pad_h+r, wo*stride_w-pad_w+s]
+ * image [batchN,C,H,W], kernel [N,C,R,S], conv [batchN,N,Hout,Wout],
+ * Hout = (H + 2 pad_h - R)/stride_h + 1. */
+int seera_hip_conv2d_fwd(const float *image, const float *kernel, float *conv,
+                         int batchN, int C, int H, int W, int N, int R, int S,
+                         int pad_h, int pad_w, int stride_h, int stride_w);
+int seera_hip_conv2d_fwd_async(const float *image, const float *kernel,
+                               float *conv, int batchN, int C, int H, int W,
+                               int N, int R, int S, int pad_h, int pad_w,
+                               int stride_h, int stride_w, void *stream);
+
+/* cuda_conv2d_bwd (convolution.cu:393-453; binding cuda_bindings.cpp:302-309).
+ * NOTE the argument order: stride before pad.
+ * dX = adjoint of conv2d_fwd in the image, dW = adjoint in the kernel. */
+int seera_hip_conv2d_bwd(const float *W, const float *X, const float *dY,
+                         float *dX, float *dW, int batch, int C, int H,
+                         int W_in, int N, int R, int S, int strideh,
+                         int stridew, int padh, int padw);
+int seera_hip_conv2d_bwd_async(const float *W, const float *X, const float *dY,
+                               float *dX, float *dW, int batch, int C, int H,
+                               int W_in, int N, int R, int S, int strideh,
+                               int stridew, int padh, int padw, void *stream);
+
+/* ---- ConvTranspose2D: engine_cuda/src/upsampling.cu ---- */
+
+/* cuda_conv2DTranpose_fwd [sic] (upsampling.cu:376-401; binding
+ * cuda_bindings.cpp:316-321). X [batch,Cin,Hin,Win], W [Cin,Cout,KH,KW],
+ * out [batch,Cout,Hout,Wout], Hout = (Hin-1)*strideh - 2 padh + KH. */
+int seera_hip_conv2DTranpose_fwd(const float *X, const float *W, float *out,
+                                 int batch, int Cin, int Hin, int Win,
+                                 int Cout, int KH, int KW, int strideh,
+                                 int stridew, int padh, int padw);
+int seera_hip_conv2DTranpose_fwd_async(const float *X, const float *W,
+                                       float *out, int batch, int Cin, int Hin,
+                                       int Win, int Cout, int KH, int KW,
+                                       int strideh, int stridew, int padh,
+                                       int padw, void *stream);
+
+/* cuda_conv2DTranspose_bwd (upsampling.cu:322-375; binding
+ * cuda_bindings.cpp:324-331). dX [batch,Cin,Hin,Win], dW [Cin,Cout,KH,KW]. */
+int seera_hip_conv2DTranspose_bwd(const float *W, const float *X,
+                                  const float *dY, float *dX, float *dW,
+                                  int batch, int Cin, int Hin, int Win,
+                                  int Cout, int KH, int KW, int strideh,
+                                  int stridew, int padh, int padw);
+int seera_hip_conv2DTranspose_bwd_async(const float *W, const float *X,
+                                        const float *dY, float *dX, float *dW,
+                                        int batch, int Cin, int Hin, int Win,
+                                        int Cout, int KH, int KW, int strideh,
+                                        int stridew, int padh, int padw,
+                                        void *stream);
+
+/* ---- timing (no reference counterpart; used by bench.py) ---- */
+
+/* Events on `stream`: create / record / elapsed milliseconds / destroy. */
+int seera_hip_event_create(void **event);
+int seera_hip_event_record(void *event, void *stream);
+int seera_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+int seera_hip_event_destroy(void *event);
+/* Create / destroy a default-priority stream. */
+int seera_hip_stream_create(void **stream);
+int seera_hip_stream_destroy(void *stream);
+int seera_hip_stream_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEERA_HIP_H */

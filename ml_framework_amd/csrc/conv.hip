@@ -1,0 +1,307 @@
+// conv.hip -- Conv2D and ConvTranspose2D forward/backward as implicit GEMMs on
+// the fp16 MFMA tile engine, with im2col / col2im folded into the operand
+// gathers (no column buffer in HBM, no atomics).
+//
+// Reference: engine_cuda/src/convolution.cu and upsampling.cu. The eight
+// reference passes reduce to three GEMM shapes:
+//   forward  out[b,f,p] = sum_{c,r,s} W[f,c,r,s] X[b,c, ho*sh-ph+r, wo*sw-pw+s]
+//            = conv2d fwd (convolution.cu:15-101, 367-389)
+//            = convT dX    (upsampling.cu:128-197, 337-346; W read [Cin,Cout,..])
+//   dgrad    out[b,c,h,w] = sum_{f,r,s} W[f,c,r,s] Y[b,f,(h+ph-r)/sh,(w+pw-s)/sw]
+//            (only taps where the division is exact and in range)
+//            = conv2d dX   (convolution.cu:144-265, 401-429)
+//            = convT fwd   (upsampling.cu:15-126, 376-401)
+//   wgrad    dW[f,c,r,s] = sum_{b,ho,wo} Y[b,f,ho,wo] X[b,c,ho*sh-ph+r,wo*sw-pw+s]
+//            = conv2d dW   (convolution.cu:268-366, 431-452)
+//            = convT dW    (upsampling.cu:202-301, 354-374; roles of X, dY swapped)
+#include "gather.h"
+#include "kernels.h"
+#include "plan.h"
+
+namespace seera {
+namespace {
+
+constexpr int kFar = 1 << 29;  // offset that fails every bounds test
+
+// Forward im2col gather: rows are output pixels q = (b, ho, wo), k = (c, r, s)
+// over the [B, C, H, W] input X.
+struct FwdGather {
+    const float* X;
+    int C, H, W, R, S, Wo, HWo, sh, sw, ph, pw, npix;
+    struct Row {
+        int64_t base;
+        int h0, w0;
+    };
+    struct Kin {
+        int64_t coff;
+        int r, s;
+    };
+    __device__ __forceinline__ Row row_info(int q) const {
+        if (q >= npix) return {0, -kFar, -kFar};
+        const int b = q / HWo, p = q - b * HWo;
+        const int ho = p / Wo, wo = p - ho * Wo;
+        return {(int64_t)b * C * H * W, ho * sh - ph, wo * sw - pw};
+    }
+    __device__ __forceinline__ Kin k_info(int k, int kmax) const {
+        if (k >= kmax) return {0, -kFar, -kFar};
+        const int rs = R * S;
+        const int c = k / rs, t = k - c * rs;
+        const int r = t / S;
+        return {(int64_t)c * H * W, r, t - r * S};
+    }
+    __device__ __forceinline__ float fetch(const Row& ro, const Kin& ki) const {
+        const int h = ro.h0 + ki.r, w = ro.w0 + ki.s;
+        if ((unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
+            return X[ro.base + ki.coff + (int64_t)h * W + w];
+        return 0.f;
+    }
+};
+
+// Transposed gather: rows are output pixels (b, h, w) of the [B, Cout, Hd, Wd]
+// result, k = (f, r, s) over the [B, F, Hi, Wi] input Y.
+struct DgradGather {
+    const float* Y;
+    int F, Hi, Wi, R, S, Wd, HWd, sh, sw, ph, pw, npix;
+    struct Row {
+        int64_t base;
+        int hp, wp;
+    };
+    struct Kin {
+        int64_t foff;
+        int r, s;
+    };
+    __device__ __forceinline__ Row row_info(int q) const {
+        if (q >= npix) return {0, -kFar, -kFar};
+        const int b = q / HWd, p = q - b * HWd;
+        const int h = p / Wd, w = p - h * Wd;
+        return {(int64_t)b * F * Hi * Wi, h + ph, w + pw};
+    }
+    __device__ __forceinline__ Kin k_info(int k, int kmax) const {
+        if (k >= kmax) return {0, kFar, kFar};
+        const int rs = R * S;
+        const int f = k / rs, t = k - f * rs;
+        const int r = t / S;
+        return {(int64_t)f * Hi * Wi, r, t - r * S};
+    }
+    __device__ __forceinline__ float fetch(const Row& ro, const Kin& ki) const {
+        const int hn = ro.hp - ki.r, wn = ro.wp - ki.s;
+        if (hn < 0 || wn < 0) return 0.f;
+        const int hi = hn / sh, wi = wn / sw;
+        if (hi * sh != hn || wi * sw != wn || hi >= Hi || wi >= Wi) return 0.f;
+        return Y[ro.base + ki.foff + (int64_t)hi * Wi + wi];
+    }
+};
+
+// Weight-gradient A operand: rows f, k = pixel q = (b, p) of Y [B, F, HWo].
+struct WgradYGather {
+    const float* Y;
+    int F, HWo;
+    struct Row {
+        int64_t foff;  // -1: row outside [0, F)
+    };
+    struct Kin {
+        int64_t off;  // -1: k outside the slice
+    };
+    __device__ __forceinline__ Row row_info(int f) const { return {f < F ? (int64_t)f * HWo : -1}; }
+    __device__ __forceinline__ Kin k_info(int q, int kmax) const {
+        if (q >= kmax) return {-1};
+        const int b = q / HWo;
+        return {(int64_t)b * F * HWo + (q - b * HWo)};
+    }
+    __device__ __forceinline__ float fetch(const Row& ro, const Kin& ki) const {
+        return (ro.foff >= 0 && ki.off >= 0) ? Y[ro.foff + ki.off] : 0.f;
+    }
+};
+
+// Weight-gradient B operand: rows (c, r, s), k = output pixel q = (b, ho, wo);
+// element X[b, c, ho*sh-ph+r, wo*sw-pw+s].
+struct WgradXGather {
+    const float* X;
+    int C, H, W, R, S, Wo, HWo, sh, sw, ph, pw, crs;
+    struct Row {
+        int64_t coff;
+        int r, s;
+    };
+    struct Kin {
+        int64_t base;
+        int h0, w0;
+    };
+    __device__ __forceinline__ Row row_info(int row) const {
+        if (row >= crs) return {0, -kFar, -kFar};
+        const int rs = R * S;
+        const int c = row / rs, t = row - c * rs;
+        const int r = t / S;
+        return {(int64_t)c * H * W, r, t - r * S};
+    }
+    __device__ __forceinline__ Kin k_info(int q, int kmax) const {
+        if (q >= kmax) return {0, -kFar, -kFar};
+        const int b = q / HWo, p = q - b * HWo;
+        const int ho = p / Wo, wo = p - ho * Wo;
+        return {(int64_t)b * C * H * W, ho * sh - ph, wo * sw - pw};
+    }
+    __device__ __forceinline__ float fetch(const Row& ro, const Kin& ki) const {
+        const int h = ki.h0 + ro.r, w = ki.w0 + ro.s;
+        if ((unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
+            return X[ki.base + ro.coff + (int64_t)h * W + w];
+        return 0.f;
+    }
+};
+
+// out[b, m, p] = sum_k Wm[m, k] * G(q = b*HW + p, k): the weights are a
+// row-major [M, K] matrix, the other operand a pixel gather, and the result an
+// NCHW tensor with M channels and HW pixels per image.
+template <int VA, class G>
+struct PixelProblem {
+    const float* Wm;
+    int64_t ldw;
+    G g;
+    float* C;
+    int out_hw;
+    int M, N, K;
+    int64_t ldc, split_stride;  // unused: this problem is never split
+    int tiles_n, k_split, gm;
+
+    template <int R, int BK, int NT>
+    using SA = StageKC<R, BK, NT, VA>;
+    template <int R, int BK, int NT>
+    using SB = StageGatherMN<R, BK, NT, G>;
+
+    template <class S>
+    __device__ __forceinline__ void init_a(S&, int, int) const {}
+    template <class S>
+    __device__ __forceinline__ void init_b(S& s, int n0, int tid) const { s.init(g, n0, tid); }
+    template <class S>
+    __device__ __forceinline__ void load_a(S& s, int m0, int k0, int k1, int tid) const {
+        s.load(Wm, ldw, m0, M, k0, k1, tid);
+    }
+    template <class S>
+    __device__ __forceinline__ void load_b(S& s, int, int k0, int k1, int tid) const {
+        s.load(g, k0, k1, tid);
+    }
+    __device__ __forceinline__ void store(int m, int n, int, float v) const {
+        const int b = n / out_hw;
+        C[((int64_t)b * M + m) * out_hw + (n - b * out_hw)] = v;
+    }
+};
+
+// dW[m, n] = sum_q Yg(m, q) * Xg(n, q), row-major output, split over q.
+struct WgradProblem {
+    WgradYGather ga;
+    WgradXGather gb;
+    float* C;
+    int M, N, K;
+    int64_t ldc, split_stride;
+    int tiles_n, k_split, gm;
+
+    template <int R, int BK, int NT>
+    using SA = StageGatherKC<R, BK, NT, WgradYGather>;
+    template <int R, int BK, int NT>
+    using SB = StageGatherKC<R, BK, NT, WgradXGather>;
+
+    template <class S>
+    __device__ __forceinline__ void init_a(S& s, int m0, int tid) const { s.init(ga, m0, tid); }
+    template <class S>
+    __device__ __forceinline__ void init_b(S& s, int n0, int tid) const { s.init(gb, n0, tid); }
+    template <class S>
+    __device__ __forceinline__ void load_a(S& s, int, int k0, int k1, int tid) const {
+        s.load(ga, k0, k1, tid);
+    }
+    template <class S>
+    __device__ __forceinline__ void load_b(S& s, int, int k0, int k1, int tid) const {
+        s.load(gb, k0, k1, tid);
+    }
+    __device__ __forceinline__ void store(int m, int n, int z, float v) const {
+        C[z * split_stride + (int64_t)m * ldc + n] = v;
+    }
+};
+
+// Wt[c, f*RS + t] = W[f, c, t]: the [F, C, R, S] weight re-laid out as a
+// row-major [C, F*R*S] matrix for the dgrad GEMM.
+__global__ void relayout_dgrad_weight(const float* __restrict__ W, float* __restrict__ Wt, int F,
+                                      int C, int RS) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n = (int64_t)F * C * RS;
+    if (i >= n) return;
+    const int t = (int)(i % RS);
+    const int64_t fc = i / RS;
+    const int c = (int)(fc % C), f = (int)(fc / C);
+    Wt[((int64_t)c * F + f) * RS + t] = W[i];
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
+             int S, int sh, int sw, int ph, int pw, hipStream_t st) {
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    const int64_t npix = (int64_t)B * Ho * Wo, K = (int64_t)C * R * S;
+    if (npix > 0x7fffffff || K > 0x7fffffff || (int64_t)B * C * H * W > (int64_t)1 << 40)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
+    if (npix == 0 || F == 0) return SEERA_OK;
+    FwdGather g{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)npix};
+    const Plan pl = plan_tiles(F, (int)npix, (int)K, true, false);
+    const bool va = aligned16(Wt) && K % 4 == 0;
+    auto fill = [&](auto p) {
+        p.Wm = Wt; p.ldw = K; p.g = g; p.C = Y; p.out_hw = Ho * Wo;
+        p.M = F; p.N = (int)npix; p.K = (int)K; p.ldc = 0; p.split_stride = 0;
+        return p;
+    };
+    if (va) return run_plan<true>(fill(PixelProblem<4, FwdGather>{}), pl, st);
+    return run_plan<true>(fill(PixelProblem<1, FwdGather>{}), pl, st);
+}
+
+int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, int Hi, int Wi,
+               int C, int H, int W, int R, int S, int sh, int sw, int ph, int pw,
+               hipStream_t st) {
+    const int64_t npix = (int64_t)B * H * W, K = (int64_t)F * R * S;
+    if (npix > 0x7fffffff || K > 0x7fffffff)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
+    if (npix == 0 || C == 0) return SEERA_OK;
+    void* ws = nullptr;
+    const int64_t wn = (int64_t)F * C * R * S;
+    SEERA_TRY(workspace(sizeof(float) * (size_t)std::max<int64_t>(wn, 1), &ws));
+    float* Wt = static_cast<float*>(ws);
+    if (wn > 0) {
+        hipLaunchKernelGGL(relayout_dgrad_weight, dim3((unsigned)((wn + 255) / 256)), dim3(256), 0,
+                           st, Wconv, Wt, F, C, R * S);
+        SEERA_HIP_TRY(hipGetLastError());
+    }
+    DgradGather g{Yin, F, Hi, Wi, R, S, W, H * W, sh, sw, ph, pw, (int)npix};
+    const Plan pl = plan_tiles(C, (int)npix, (int)K, true, false);
+    auto fill = [&](auto p) {
+        p.Wm = Wt; p.ldw = K; p.g = g; p.C = out; p.out_hw = H * W;
+        p.M = C; p.N = (int)npix; p.K = (int)K; p.ldc = 0; p.split_stride = 0;
+        return p;
+    };
+    if (K % 4 == 0) return run_plan<true>(fill(PixelProblem<4, DgradGather>{}), pl, st);
+    return run_plan<true>(fill(PixelProblem<1, DgradGather>{}), pl, st);
+}
+
+int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
+               int R, int S, int sh, int sw, int ph, int pw, hipStream_t st) {
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    const int64_t npix = (int64_t)B * Ho * Wo, crs = (int64_t)C * R * S;
+    if (npix > 0x7fffffff || crs > 0x7fffffff)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
+    if (F == 0 || crs == 0) return SEERA_OK;
+    WgradProblem p{};
+    p.ga = WgradYGather{Y, F, Ho * Wo};
+    p.gb = WgradXGather{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)crs};
+    p.C = dW;
+    p.M = F;
+    p.N = (int)crs;
+    p.K = (int)npix;
+    p.ldc = crs;
+    p.split_stride = 0;
+    if (npix == 0) {
+        // Empty contraction: dW = 0.
+        SEERA_HIP_TRY(hipMemsetAsync(dW, 0, sizeof(float) * (size_t)F * crs, st));
+        return SEERA_OK;
+    }
+    // Gathers only: the 64x64 tile, split over pixels.
+    const Plan pl = plan_tiles(F, (int)crs, (int)npix, false, true);
+    return run_plan<false>(p, pl, st);
+}
+
+}  // namespace seera

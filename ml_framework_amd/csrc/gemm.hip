@@ -1,0 +1,152 @@
+// gemm.hip -- GEMM forward / backward and transposes for gfx950.
+//
+// Reference: engine_cuda/src/GEMM.cu. The reference runs one 32-lane warp
+// per 16x16 output tile and, for the backward, materialises B^T and A^T and
+// loops over the batch on the host (GEMM.cu:164-225). Here:
+//   forward  C = A.B        one GEMM with M' = Nbatch*M (A is contiguous
+//                           [Nbatch*M, K] and B is shared), B read N-major
+//   dA = dC.B^T             one GEMM, B^T read straight from B (K-major)
+//   dB = sum_b A_b^T.dC_b   one GEMM with K' = Nbatch*M, A^T read straight
+//                           from A; split-K with a deterministic reduce
+// No transposed copies and no host loop.
+#include <algorithm>
+
+#include "kernels.h"
+#include "plan.h"
+
+namespace seera {
+namespace {
+
+// Strided fp32 matrix view with an element layout: K-contiguous (KC) means
+// element (row, k) at ptr[row*ld + k]; otherwise at ptr[k*ld + row].
+template <bool KC, int VEC>
+struct Operand {
+    template <int ROWS, int BK, int NT>
+    using Stager = typename std::conditional<KC, StageKC<ROWS, BK, NT, VEC>,
+                                             StageMNC<ROWS, BK, NT, VEC>>::type;
+};
+
+template <bool A_KC, int VA, bool B_KC, int VB>
+struct GemmProblem {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    int64_t lda, ldb, ldc;
+    int64_t split_stride;  // distance between split-K partial outputs
+    int tiles_n, k_split, gm;
+
+    template <int R, int BK, int NT>
+    using SA = typename Operand<A_KC, VA>::template Stager<R, BK, NT>;
+    template <int R, int BK, int NT>
+    using SB = typename Operand<B_KC, VB>::template Stager<R, BK, NT>;
+
+    template <class S>
+    __device__ __forceinline__ void load_a(S& s, int m0, int k0, int k1, int tid) const {
+        s.load(A, lda, m0, M, k0, k1, tid);
+    }
+    template <class S>
+    __device__ __forceinline__ void load_b(S& s, int n0, int k0, int k1, int tid) const {
+        s.load(B, ldb, n0, N, k0, k1, tid);
+    }
+    template <class S>
+    __device__ __forceinline__ void init_a(S&, int, int) const {}
+    template <class S>
+    __device__ __forceinline__ void init_b(S&, int, int) const {}
+    __device__ __forceinline__ void store(int m, int n, int z, float v) const {
+        C[z * split_stride + (int64_t)m * ldc + n] = v;
+    }
+};
+
+__global__ void fill_zero_2d(float* __restrict__ C, int M, int N, int64_t ldc) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (int64_t)M * N) C[(i / N) * ldc + i % N] = 0.f;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Dispatch on operand vector-load eligibility. Only the 64x64 tile carries the
+// scalar (any shape / alignment) variants.
+template <bool A_KC, bool B_KC>
+int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                  int64_t ldc, int M, int N, int K, hipStream_t st) {
+    if (M == 0 || N == 0) return SEERA_OK;
+    if (K == 0) {
+        // Empty contraction: C = 0 (the reference's K loop never runs).
+        const int64_t n = (int64_t)M * N;
+        hipLaunchKernelGGL(fill_zero_2d, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           C, M, N, ldc);
+        SEERA_HIP_TRY(hipGetLastError());
+        return SEERA_OK;
+    }
+    const bool va = aligned16(A) && lda % 4 == 0 && (A_KC ? K : M) % 4 == 0;
+    const bool vb = aligned16(B) && ldb % 4 == 0 && (B_KC ? K : N) % 4 == 0;
+    const Plan pl = plan_tiles(M, N, K, va && vb, true);
+    auto fill = [&](auto prob) {
+        prob.A = A; prob.B = B; prob.C = C;
+        prob.M = M; prob.N = N; prob.K = K;
+        prob.lda = lda; prob.ldb = ldb; prob.ldc = ldc;
+        prob.split_stride = 0;
+        return prob;
+    };
+    if (va && vb) return run_plan<true>(fill(GemmProblem<A_KC, 4, B_KC, 4>{}), pl, st);
+    if (va) return run_plan<false>(fill(GemmProblem<A_KC, 4, B_KC, 1>{}), pl, st);
+    if (vb) return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 4>{}), pl, st);
+    return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1>{}), pl, st);
+}
+
+// LDS-tiled transpose of one [rows, cols] slice per blockIdx.z; 64x64 tiles,
+// coalesced reads and writes, +1 padding against bank conflicts.
+__global__ __launch_bounds__(256) void transpose_tiles(const float* __restrict__ in,
+                                                       float* __restrict__ out, int rows,
+                                                       int cols) {
+    __shared__ float t[64][65];
+    const int64_t slice = (int64_t)rows * cols;
+    in += blockIdx.z * slice;
+    out += blockIdx.z * slice;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) t[i][tx] = in[(int64_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) out[(int64_t)c * rows + r] = t[tx][i];
+    }
+}
+
+}  // namespace
+
+int gemm_fwd(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch,
+             hipStream_t st) {
+    const int64_t Mb = (int64_t)M * Nbatch;
+    if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    // A [Mb, K] row-major (K-contiguous), B [K, N] row-major (N-contiguous).
+    return gemm_dispatch<true, false>(A, K, B, N, C, N, (int)Mb, N, K, st);
+}
+
+int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M,
+             int N, int K, int Nbatch, hipStream_t st) {
+    const int64_t Mb = (int64_t)M * Nbatch;
+    if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    // dA [Mb, K] = dC [Mb, N] . B^T : B^T element (k, n) = B[k*N + n] is
+    // K-contiguous in the GEMM's contraction index n.
+    SEERA_TRY((gemm_dispatch<true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st)));
+    // dB [K, N] = A^T [K, Mb] . dC [Mb, N]: A^T element (k, m) = A[m*K + k]
+    // is M-contiguous in the output row index k.
+    return gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st);
+}
+
+int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st) {
+    if (batch == 0 || rows == 0 || cols == 0) return SEERA_OK;
+    dim3 grid((cols + 63) / 64, (rows + 63) / 64, batch);
+    if (grid.y > 65535 || grid.z > 65535)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "transpose extent too large");
+    hipLaunchKernelGGL(transpose_tiles, grid, dim3(256), 0, st, in, out, rows, cols);
+    SEERA_HIP_TRY(hipGetLastError());
+    return SEERA_OK;
+}
+
+}  // namespace seera

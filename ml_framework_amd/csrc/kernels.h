@@ -1,0 +1,28 @@
+// kernels.h -- internal (C++) entry points of the HIP kernels. All enqueue on
+// `st` without synchronizing and return a SEERA_* status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace seera {
+
+// C[Mb, N] = A[Mb, K] . B[K, N] with Mb = M * Nbatch.
+int gemm_fwd(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch,
+             hipStream_t st);
+// dA = dC . B^T, dB = A^T . dC over the folded batch.
+int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M, int N,
+             int K, int Nbatch, hipStream_t st);
+// out[b, c, r] = in[b, r, c] for b < batch.
+int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st);
+
+// Y[B, F, Ho, Wo] = conv(X[B, C, H, W], Wt[F, C, R, S]).
+int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
+             int S, int sh, int sw, int ph, int pw, hipStream_t st);
+// out[B, C, H, W] = transposed conv of Y[B, F, Hi, Wi] with W[F, C, R, S].
+int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, int Hi, int Wi,
+               int C, int H, int W, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
+// dW[F, C, R, S] = sum over (b, ho, wo) of Y[B, F, Ho, Wo] x im2col(X[B, C, H, W]).
+int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
+               int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
+
+}  // namespace seera

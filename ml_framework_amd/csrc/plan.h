@@ -1,0 +1,116 @@
+// plan.h -- tile-shape choice, split-K and launch for igemm problems.
+#pragma once
+
+#include <algorithm>
+
+#include "igemm.h"
+#include "runtime.h"
+
+namespace seera {
+
+// Block-tile shapes (BM x BN, BK = 32):
+//   L   256x256, 2x2 waves of 128x128   large square GEMMs
+//   W   64x256,  1x4 waves of 64x64     few rows (conv output channels)
+//   M   128x128, 2x2 waves of 64x64
+//   S   64x64,   2x2 waves of 32x32     small / odd shapes, scalar loads
+enum class Tile { L, W, M, S };
+
+struct Plan {
+    Tile tile;
+    int splits;
+    int k_split;
+};
+
+constexpr int kNumCUs = 256;
+constexpr int kBK = 32;
+
+inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
+inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
+
+inline int64_t tile_count(Tile t, int M, int N) {
+    return (int64_t)((M + tile_bm(t) - 1) / tile_bm(t)) * ((N + tile_bn(t) - 1) / tile_bn(t));
+}
+
+// Padded work per CU (rounds of a full chip x tile area), weighted by how
+// efficiently each tile shape feeds the matrix cores; lowest wins.
+inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split) {
+    Tile cands[4] = {Tile::L, Tile::W, Tile::M, Tile::S};
+    const double eff[4] = {1.0, 1.2, 1.2, 1.6};
+    Plan best{Tile::S, 1, std::max(K, 1)};
+    double best_cost = 1e300;
+    for (int i = 0; i < 4; ++i) {
+        const Tile t = cands[i];
+        if (!big_tiles && t != Tile::S) continue;
+        const int64_t tiles = tile_count(t, M, N);
+        const double rounds = (double)((tiles + kNumCUs - 1) / kNumCUs);
+        const double cost = rounds * tile_bm(t) * tile_bn(t) * eff[i];
+        if (cost < best_cost) {
+            best_cost = cost;
+            best.tile = t;
+        }
+    }
+    const int64_t tiles = tile_count(best.tile, M, N);
+    if (allow_split && tiles < kNumCUs / 2 && K >= 8 * kBK) {
+        int want = (int)std::min<int64_t>((kNumCUs + tiles - 1) / tiles, K / (4 * kBK));
+        want = std::max(want, 1);
+        int ks = (K + want - 1) / want;
+        ks = (ks + kBK - 1) / kBK * kBK;
+        best.splits = (K + ks - 1) / ks;
+        best.k_split = ks;
+    }
+    return best;
+}
+
+// Deterministic split-K reduction: C[m, n] = sum_z P[z][m][n] in z order.
+static __global__ void splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
+                                     int M, int N, int64_t ldc, int splits, int64_t stride) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * N) return;
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += P[z * stride + i];
+    C[(i / N) * ldc + i % N] = s;
+}
+
+template <bool BIG, class P>
+hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
+    if constexpr (BIG) {
+        switch (t) {
+            case Tile::L: return launch_igemm<256, 256, 32, 2, 2>(p, splits, st);
+            case Tile::W: return launch_igemm<64, 256, 32, 1, 4>(p, splits, st);
+            case Tile::M: return launch_igemm<128, 128, 32, 2, 2>(p, splits, st);
+            default: break;
+        }
+    }
+    return launch_igemm<64, 64, 32, 2, 2>(p, splits, st);
+}
+
+// Runs problem `p` under plan `pl`. Problems that support split-K expose
+// `C`, `ldc` and `split_stride` and a row-major store; `splittable` says so.
+template <bool BIG, class P>
+int run_plan(P p, const Plan& pl, hipStream_t st) {
+    p.tiles_n = (p.N + tile_bn(pl.tile) - 1) / tile_bn(pl.tile);
+    p.k_split = pl.splits > 1 ? pl.k_split : std::max(p.K, 1);
+    p.gm = 4;
+    if (tile_count(pl.tile, p.M, p.N) > kMaxGridX)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "grid too large (%d x %d)", p.M, p.N);
+    float* final_c = p.C;
+    const int64_t final_ld = p.ldc;
+    if (pl.splits > 1) {
+        void* ws = nullptr;
+        SEERA_TRY(workspace(sizeof(float) * (size_t)pl.splits * p.M * p.N, &ws));
+        p.C = static_cast<float*>(ws);
+        p.ldc = p.N;
+        p.split_stride = (int64_t)p.M * p.N;
+    }
+    hipError_t e = launch_tile<BIG>(p, pl.tile, pl.splits, st);
+    if (e != hipSuccess) return fail_hip(e, "igemm launch");
+    if (pl.splits > 1) {
+        const int64_t n = (int64_t)p.M * p.N;
+        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride);
+        SEERA_HIP_TRY(hipGetLastError());
+    }
+    return SEERA_OK;
+}
+
+}  // namespace seera

@@ -1,0 +1,185 @@
+// seera_cuda_module.cpp -- the `seera_cuda` Python module: the reference's
+// function names and signatures (engine_cuda/src/cuda_bindings.cpp:14-533)
+// over the C ABI of include/seera_hip.h. Device pointers cross as Python ints
+// (uintptr_t), dims as C ints, exactly as cuTen.py and Seera_Engine.py pass
+// them. A failing call raises RuntimeError (the reference ignores errors).
+//
+// Host-only translation unit: no HIP headers, no GPU code.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "seera_hip.h"
+
+namespace py = pybind11;
+
+using arr_f = py::array_t<float, py::array::c_style | py::array::forcecast>;
+using arr_i = py::array_t<int32_t, py::array::c_style | py::array::forcecast>;
+using arr_s = py::array_t<int16_t, py::array::c_style | py::array::forcecast>;
+
+namespace {
+
+void check(int status) {
+    if (status != SEERA_OK)
+        throw std::runtime_error(std::string("seera_cuda: ") + seera_hip_last_error());
+}
+
+template <class T>
+T* dev(uintptr_t p) {
+    return reinterpret_cast<T*>(p);
+}
+
+uintptr_t alloc_bytes(size_t n) {
+    void* p = nullptr;
+    check(seera_hip_malloc(&p, n));
+    return reinterpret_cast<uintptr_t>(p);
+}
+
+std::vector<ssize_t> dims_of(const py::tuple& shape, size_t* count) {
+    std::vector<ssize_t> dims;
+    size_t n = 1;
+    for (auto s : shape) {
+        const ssize_t d = s.cast<ssize_t>();
+        if (d < 0) throw std::invalid_argument("seera_cuda: negative extent in shape");
+        dims.push_back(d);
+        n *= (size_t)d;
+    }
+    *count = n;
+    return dims;
+}
+
+template <class T, class Arr>
+uintptr_t upload(const Arr& a) {
+    const size_t bytes = (size_t)a.size() * sizeof(T);
+    const uintptr_t p = alloc_bytes(bytes);
+    check(seera_hip_memcpy_h2d(dev<void>(p), a.data(), bytes));
+    return p;
+}
+
+template <class T>
+py::array_t<T> download(uintptr_t ptr, const py::tuple& shape) {
+    size_t n = 0;
+    std::vector<ssize_t> dims = dims_of(shape, &n);
+    py::array_t<T> out(dims);
+    check(seera_hip_memcpy_d2h(out.mutable_data(), dev<const void>(ptr), n * sizeof(T)));
+    return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(seera_cuda, m) {
+    m.doc() = "Seera GEMM/conv hot path on MI355X (gfx950): fp16 MFMA, fp32 accumulate";
+
+    // ---- memory management (cuda_bindings.cpp:23-66) ----
+    m.def("cuda_malloc", [](size_t n_bytes) { return alloc_bytes(n_bytes); },
+          "Allocate n bytes on the GPU, returns the device address");
+    m.def("cuda_malloc_f16", [](int n) { return alloc_bytes((size_t)n * sizeof(float)); },
+          "Allocate n float elements (the reference stores fp32 here too)");
+    m.def("cuda_malloc_f32", [](int n) { return alloc_bytes((size_t)n * sizeof(float)); },
+          "Allocate n float32 elements on the GPU");
+    m.def("cuda_malloc_i32", [](int n) { return alloc_bytes((size_t)n * sizeof(int32_t)); },
+          "Allocate n int32 elements on the GPU");
+    m.def("cuda_malloc_i16", [](int n) { return alloc_bytes((size_t)n * sizeof(int16_t)); },
+          "Allocate n int16 elements on the GPU");
+    m.def("cuda_free", [](uintptr_t p) { check(seera_hip_free(dev<void>(p))); },
+          "Free GPU memory");
+    m.def("cuda_memcopy_devicetodevice",
+          [](uintptr_t dst, uintptr_t src, int num_elem) {
+              check(seera_hip_memcpy_d2d(dev<void>(dst), dev<const void>(src),
+                                         (size_t)num_elem * sizeof(float)));
+          },
+          "Copy num_elem floats from ptr2 to ptr1 on the GPU");
+    m.def("cuda_memset",
+          [](uintptr_t p, int value, size_t n_bytes) {
+              check(seera_hip_memset(dev<void>(p), value, n_bytes));
+          },
+          "Memset GPU memory");
+
+    // ---- transfers (cuda_bindings.cpp:73-170) ----
+    m.def("to_device_f16", [](arr_f a) { return upload<float>(a); },
+          "Upload float32 numpy -> float32 GPU buffer (reference name)");
+    m.def("to_host_f16", [](uintptr_t p, py::tuple s) { return download<float>(p, s); },
+          "Download float32 GPU buffer -> numpy with shape (reference name)");
+    m.def("to_device_f32", [](arr_f a) { return upload<float>(a); },
+          "Upload float32 numpy -> float32 GPU buffer");
+    m.def("to_host_f32", [](uintptr_t p, py::tuple s) { return download<float>(p, s); },
+          "Download float32 GPU buffer -> numpy with shape");
+    m.def("to_host_i32", [](uintptr_t p, py::tuple s) { return download<int32_t>(p, s); },
+          "Download int32 GPU buffer -> numpy with shape");
+    m.def("to_host_i16", [](uintptr_t p, py::tuple s) { return download<int16_t>(p, s); },
+          "Download int16 GPU buffer -> numpy with shape");
+    m.def("to_device_i16", [](arr_s a) { return upload<int16_t>(a); },
+          "Upload int16 numpy -> GPU buffer");
+    m.def("to_device_i32", [](arr_i a) { return upload<int32_t>(a); },
+          "Upload int32 numpy -> GPU buffer");
+
+    // ---- matmul (cuda_bindings.cpp:260-287) ----
+    m.def("cuda_matmul",
+          [](uintptr_t A, uintptr_t B, uintptr_t C, int M, int N, int K, int Nbatch) {
+              check(seera_hip_matmul(dev<const float>(A), dev<const float>(B), dev<float>(C), M,
+                                     N, K, Nbatch));
+          },
+          "Matmul: C[Nbatch,M,N] = A[Nbatch,M,K] @ B[K,N] (GPU ptrs)");
+    m.def("cuda_matmul_bwd",
+          [](uintptr_t A, uintptr_t B, uintptr_t dC, uintptr_t dA, uintptr_t dB, int M, int N,
+             int K, int Nbatch) {
+              check(seera_hip_matmul_bwd(dev<const float>(A), dev<const float>(B),
+                                         dev<const float>(dC), dev<float>(dA), dev<float>(dB), M,
+                                         N, K, Nbatch));
+          },
+          "Matmul backward: dA = dC @ B^T, dB = sum_b A_b^T @ dC_b (GPU ptrs)");
+    m.def("cuda_transpose_2d",
+          [](uintptr_t in, uintptr_t out, int rows, int cols) {
+              check(seera_hip_transpose_2d(dev<const float>(in), dev<float>(out), rows, cols));
+          },
+          "Transpose 2D: in[rows,cols] -> out[cols,rows] (GPU ptrs)");
+    m.def("cuda_transpose_3d",
+          [](uintptr_t in, uintptr_t out, int Nbatch, int M, int K) {
+              check(seera_hip_transpose_3d(dev<const float>(in), dev<float>(out), Nbatch, M, K));
+          },
+          "Transpose 3D batched: in[Nbatch,M,K] -> out[Nbatch,K,M] (GPU ptrs)");
+
+    // ---- Conv2D (cuda_bindings.cpp:294-309) ----
+    m.def("cuda_conv2d_fwd",
+          [](uintptr_t image, uintptr_t kernel, uintptr_t conv, int batchN, int C, int H, int W,
+             int N, int R, int S, int pad_h, int pad_w, int stride_h, int stride_w) {
+              check(seera_hip_conv2d_fwd(dev<const float>(image), dev<const float>(kernel),
+                                         dev<float>(conv), batchN, C, H, W, N, R, S, pad_h, pad_w,
+                                         stride_h, stride_w));
+          },
+          "Conv2D forward (GPU ptrs); note pad before stride");
+    m.def("cuda_conv2d_bwd",
+          [](uintptr_t W, uintptr_t X, uintptr_t dY, uintptr_t dX, uintptr_t dW, int batch, int C,
+             int H, int W_in, int N, int R, int S, int strideh, int stridew, int padh, int padw) {
+              check(seera_hip_conv2d_bwd(dev<const float>(W), dev<const float>(X),
+                                         dev<const float>(dY), dev<float>(dX), dev<float>(dW),
+                                         batch, C, H, W_in, N, R, S, strideh, stridew, padh,
+                                         padw));
+          },
+          "Conv2D backward (GPU ptrs); note stride before pad");
+
+    // ---- ConvTranspose2D (cuda_bindings.cpp:316-331) ----
+    m.def("cuda_conv2DTranpose_fwd",
+          [](uintptr_t X, uintptr_t W, uintptr_t out, int batch, int Cin, int Hin, int Win,
+             int Cout, int KH, int KW, int strideh, int stridew, int padh, int padw) {
+              check(seera_hip_conv2DTranpose_fwd(dev<const float>(X), dev<const float>(W),
+                                                 dev<float>(out), batch, Cin, Hin, Win, Cout, KH,
+                                                 KW, strideh, stridew, padh, padw));
+          },
+          "ConvTranspose2D forward (GPU ptrs)");
+    m.def("cuda_conv2DTranspose_bwd",
+          [](uintptr_t W, uintptr_t X, uintptr_t dY, uintptr_t dX, uintptr_t dW, int batch,
+             int Cin, int Hin, int Win, int Cout, int KH, int KW, int strideh, int stridew,
+             int padh, int padw) {
+              check(seera_hip_conv2DTranspose_bwd(dev<const float>(W), dev<const float>(X),
+                                                  dev<const float>(dY), dev<float>(dX),
+                                                  dev<float>(dW), batch, Cin, Hin, Win, Cout, KH,
+                                                  KW, strideh, stridew, padh, padw));
+          },
+          "ConvTranspose2D backward (GPU ptrs)");
+}

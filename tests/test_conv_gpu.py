@@ -1,0 +1,123 @@
+"""Conv2D and ConvTranspose2D forward/backward on the GPU, through the C ABI,
+against the oracle (seera_cpp restatement) on the same seeded inputs: the
+reference's own test shapes (Testing/test_1.py, test_3.py) and BASELINE
+configs 4 and 5 at full size. Tolerance as in test_gemm_gpu.py."""
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle
+from ml_framework_amd import capi
+from oracle import fp16r
+from tests.helpers import (assert_parity, hip_conv_bwd, hip_conv_fwd, hip_convT_bwd,
+                           hip_convT_fwd, rel_fro)
+from tests.shapes import CONV2D, CONVT
+
+pytestmark = pytest.mark.gpu
+S = oracle.seera_cpp
+STRICT = 1e-5
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _gpu():
+    assert capi.gpu_available(), "no HIP device visible"
+
+
+def _kaiming(r, shape, fan_in):
+    lim = np.sqrt(6.0 / fan_in)
+    return r.uniform(-lim, lim, shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("case", CONV2D, ids=[c[0] for c in CONV2D])
+def test_conv2d_parity(case):
+    name, N, C, H, W, F, KH, KW, s, p = case
+    r = np.random.default_rng(zlib.crc32(name.encode()))
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = _kaiming(r, (F, C, KH, KW), C * KH * KW)
+    y = hip_conv_fwd(x, w, s, p)
+    ry = S.conv2d_forward(fp16r(x), fp16r(w), s, s, p, p)
+    assert_parity(y, ry, f"{name} fwd")
+    assert rel_fro(y, ry) <= STRICT
+    dy = r.standard_normal(ry.shape).astype(np.float32)
+    dx, dw = hip_conv_bwd(dy, x, w, s, p)
+    rdx, rdw = S.conv2d_backward(fp16r(dy), fp16r(x), fp16r(w), s, s, p, p)
+    assert_parity(dx, rdx, f"{name} dX")
+    assert_parity(dw, rdw, f"{name} dW")
+    assert rel_fro(dx, rdx) <= STRICT and rel_fro(dw, rdw) <= STRICT
+
+
+@pytest.mark.parametrize("case", CONVT, ids=[c[0] for c in CONVT])
+def test_convT_parity(case):
+    name, N, Cin, H, W, Cout, KH, KW, s, p = case
+    r = np.random.default_rng(zlib.crc32(name.encode()))
+    x = r.standard_normal((N, Cin, H, W)).astype(np.float32)
+    w = _kaiming(r, (Cin, Cout, KH, KW), Cin * KH * KW)
+    y = hip_convT_fwd(x, w, s, p)
+    ry = S.conv_transpose2d_forward(fp16r(x), fp16r(w), s, s, p, p)
+    assert_parity(y, ry, f"{name} fwd")
+    assert rel_fro(y, ry) <= STRICT
+    dy = r.standard_normal(ry.shape).astype(np.float32)
+    dx, dw = hip_convT_bwd(dy, x, w, s, p)
+    rdx, rdw = S.conv_transpose2d_backward(fp16r(dy), fp16r(x), fp16r(w), s, s, p, p)
+    assert_parity(dx, rdx, f"{name} dX")
+    assert_parity(dw, rdw, f"{name} dW")
+    assert rel_fro(dx, rdx) <= STRICT and rel_fro(dw, rdw) <= STRICT
+
+
+def _inner(a, b):
+    return float(np.sum(np.asarray(a, np.float64) * np.asarray(b, np.float64)))
+
+
+def test_conv2d_config4_full():
+    """N=128, 64->64, 56x56, 3x3 s1 p1, seed 0."""
+    r = np.random.default_rng(0)
+    x = fp16r(r.standard_normal((128, 64, 56, 56)))
+    w = fp16r(_kaiming(r, (64, 64, 3, 3), 576))
+    dy = fp16r(r.standard_normal((128, 64, 56, 56)))
+    y = hip_conv_fwd(x, w, 1, 1)
+    assert_parity(y, S.conv2d_forward(x, w, 1, 1, 1, 1), "cfg4 fwd")
+    dx, dw = hip_conv_bwd(dy, x, w, 1, 1)
+    rdx, rdw = S.conv2d_backward(dy, x, w, 1, 1, 1, 1)
+    assert_parity(dx, rdx, "cfg4 dX")
+    assert_parity(dw, rdw, "cfg4 dW")
+    ref = _inner(y, dy)
+    assert abs(_inner(x, dx) - ref) <= 1e-4 * abs(ref) + 1.0
+    assert abs(_inner(w, dw) - ref) <= 1e-4 * abs(ref) + 1.0
+
+
+def test_convT_config5_full():
+    """N=32, 128->64, 28x28 -> 56x56, 4x4 s2 p1, seed 0."""
+    r = np.random.default_rng(0)
+    x = fp16r(r.standard_normal((32, 128, 28, 28)))
+    w = fp16r(_kaiming(r, (128, 64, 4, 4), 2048))
+    dy = fp16r(r.standard_normal((32, 64, 56, 56)))
+    y = hip_convT_fwd(x, w, 2, 1)
+    assert_parity(y, S.conv_transpose2d_forward(x, w, 2, 2, 1, 1), "cfg5 fwd")
+    dx, dw = hip_convT_bwd(dy, x, w, 2, 1)
+    rdx, rdw = S.conv_transpose2d_backward(dy, x, w, 2, 2, 1, 1)
+    assert_parity(dx, rdx, "cfg5 dX")
+    assert_parity(dw, rdw, "cfg5 dW")
+    ref = _inner(y, dy)
+    assert abs(_inner(x, dx) - ref) <= 1e-4 * abs(ref) + 1.0
+    assert abs(_inner(w, dw) - ref) <= 1e-4 * abs(ref) + 1.0
+
+
+def test_outputs_are_overwritten_not_accumulated():
+    """dX and dW are overwritten (the Python layer accumulates; Seera_Engine.py:339-340)."""
+    from ml_framework_amd.capi import DeviceBuffer
+    r = np.random.default_rng(9)
+    x = r.standard_normal((2, 3, 8, 8)).astype(np.float32)
+    w = r.standard_normal((4, 3, 3, 3)).astype(np.float32)
+    dy = r.standard_normal((2, 4, 8, 8)).astype(np.float32)
+    ref = hip_conv_bwd(dy, x, w, 1, 1)
+    with DeviceBuffer.from_array(w) as pw, DeviceBuffer.from_array(x) as px, \
+            DeviceBuffer.from_array(dy) as pdy, DeviceBuffer(x.nbytes) as pdx, \
+            DeviceBuffer(w.nbytes) as pdw:
+        pdx.fill(0x7F)
+        pdw.fill(0x7F)
+        for _ in range(2):
+            capi.call("seera_hip_conv2d_bwd", pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr,
+                      2, 3, 8, 8, 4, 3, 3, 1, 1, 1, 1)
+        assert np.array_equal(pdx.to_array(x.shape), ref[0])
+        assert np.array_equal(pdw.to_array(w.shape), ref[1])
