@@ -79,9 +79,21 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
         SEERA_HIP_TRY(hipGetLastError());
         return SEERA_OK;
     }
+    // Tile loads address one tile through a buffer resource with 32-bit
+    // offsets: the largest tile's span must stay below kMaxTileSpanBytes, else
+    // only the 64x64 tile is used, and past that the shape is rejected.
+    auto span = [](bool kc, int rows, int64_t ld) {
+        return kc ? span_kc(rows, kMaxBK, ld) : span_mnc(rows, kMaxBK, ld);
+    };
+    const bool big_ok = span(A_KC, 256, lda) < kMaxTileSpanBytes &&
+                        span(B_KC, 256, ldb) < kMaxTileSpanBytes;
+    if (span(A_KC, 64, lda) >= kMaxTileSpanBytes || span(B_KC, 64, ldb) >= kMaxTileSpanBytes)
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "GEMM leading dimension too large for 32-bit tile offsets (lda=%lld ldb=%lld)",
+                    (long long)lda, (long long)ldb);
     const bool va = aligned16(A) && lda % 4 == 0 && (A_KC ? K : M) % 4 == 0;
     const bool vb = aligned16(B) && ldb % 4 == 0 && (B_KC ? K : N) % 4 == 0;
-    const Plan pl = plan_tiles(M, N, K, va && vb, true);
+    const Plan pl = plan_tiles(M, N, K, va && vb && big_ok, true);
     auto fill = [&](auto prob) {
         prob.A = A; prob.B = B; prob.C = C;
         prob.M = M; prob.N = N; prob.K = K;

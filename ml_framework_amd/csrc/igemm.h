@@ -11,10 +11,11 @@
 //   p.M, p.N, p.K, p.tiles_n, p.k_split, p.gm
 // gridDim.x = tiles_m * tiles_n, gridDim.z = number of K splits.
 //
-// Pipeline: the next BK slice is loaded from HBM into registers while the
-// matrix cores consume the current slice from LDS; the registers are then
-// converted to fp16 and written to the other LDS buffer (one barrier per
-// slice).
+// Pipeline (one barrier per BK slice, two LDS stages): the loads of slice t+1
+// are issued from HBM into registers before the matrix cores start on slice t
+// (held in LDS stage t&1); while the MFMAs of k-step kk run, the LDS fragments
+// of k-step kk+1 are read; after the last MFMA of slice t the registers are
+// rounded to fp16 and written to the other stage.
 #pragma once
 
 #include "mfma_core.h"
@@ -29,6 +30,7 @@ struct TileCfg {
     static constexpr int LDS_BYTES = 2 * (BM + BN) * BK * 2;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold one 32x32 MFMA tile");
     static_assert(BM % (WM * 32) == 0 && BN % (WN * 32) == 0, "tile/wave mismatch");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS tile exceeds the 160 KB of a gfx950 CU");
 };
 
 template <int BM, int BN, int BK, int WM, int WN, class P>

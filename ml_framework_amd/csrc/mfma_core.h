@@ -8,8 +8,13 @@
 // LDS layout: each operand tile is stored "K-contiguous", one row per M (or N)
 // index holding BK fp16 values, so that one 16-byte ds_read_b128 gives a lane
 // the 8 consecutive k values that v_mfma_f32_32x32x16_f16 expects. The 16-byte
-// chunks of a row are XOR-swizzled by the row index so that the 32 lanes
-// reading 32 consecutive rows at the same k spread over all LDS banks.
+// chunks of a row are XOR-swizzled by the row index so that the lanes reading
+// consecutive rows at the same k spread over all LDS banks.
+//
+// Global loads go through buffer resources: a lane whose element lies outside
+// the tensor (edge tiles, K tails) gets an offset past the resource's
+// num_records and the hardware returns 0 for it, so predication costs one
+// v_cndmask instead of a branch per load.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -37,15 +42,60 @@ __device__ __forceinline__ floatx16 mfma32x32x16(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// Buffer-resource loads. A resource covers kBufRecords bytes from its base;
+// offsets at or beyond kBufOOB read as 0. Callers keep every in-range offset
+// below kBufOOB (the host checks tile spans against kMaxTileSpanBytes).
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kBufRecords = 0x7FFFFF00u;
+constexpr uint32_t kBufOOB = 0x7FFFFF00u;
+constexpr int64_t kMaxTileSpanBytes = 0x7F000000ll;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
+    // Word 3 = 0x00020000: raw (untyped) 32-bit data format, no swizzle.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kBufRecords,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ floatx4 buf_load4(rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_load1(rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile addressing.
+// ---------------------------------------------------------------------------
+
 // Element offset (in halves) of 16-byte chunk `chunk` of row `row` in a tile
 // whose rows hold BK halves.
+//
+// A 128-byte window covers all 32 banks as eight 16-byte slots, and a wave's
+// ds_read/write_b128 is served eight lanes at a time, so eight lanes must hit
+// eight distinct slots. Three access patterns occur:
+//   MFMA fragment reads   8 consecutive rows, one chunk
+//   K-contiguous stores   consecutive lanes fill the chunks of consecutive rows
+//   transposed stores     rows 4g+q for 8 consecutive g, one chunk and q
+// BK=64: one row per window, slot = chunk ^ f(row) with f's three bits
+//   (r0^r3, r1^r4, r2): a bijection in (r0,r1,r2) for the reads and in
+//   (r2,r3,r4) for the transposed stores.
+// BK=32: rows 2j and 2j+1 share window j, slot = (4*(row&1) + chunk) ^ f(j)
+//   with f(j) = (j0^j2, j1, j3): its low two bits are a bijection in (j0,j1)
+//   for the reads and all three bits one in (j1,j2,j3) for the stores.
 template <int BK>
 __device__ __forceinline__ int lds_off(int row, int chunk) {
     static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
-    // BK=32: a row is 64 B, two rows share a 128-byte bank window, so the
-    // swizzle key changes every second row; BK=64: one row per window.
-    const int key = BK == 32 ? ((row >> 1) & 3) : (row & 7);
-    return row * BK + ((chunk ^ key) << 3);
+    if constexpr (BK == 64) {
+        const int f = ((row ^ (row >> 3)) & 3) | (row & 4);
+        return row * 64 + ((chunk ^ f) << 3);
+    } else {
+        const int j = row >> 1;
+        const int f = ((j ^ (j >> 2)) & 1) | (j & 2) | ((j >> 1) & 4);
+        return j * 64 + (((((row & 1) << 2) | chunk) ^ f) << 3);
+    }
 }
 
 template <int BK>
@@ -60,7 +110,8 @@ __device__ __forceinline__ void lds_write8(half_t* tile, int row, int chunk, hal
 
 // ---------------------------------------------------------------------------
 // Operand stagers: global fp32 -> registers (load) -> fp16 LDS tile (store).
-// A stager covers a tile of ROWS (M or N) x BK (K) elements.
+// A stager covers a tile of ROWS (M or N) x BK (K) elements starting at
+// (r0, k0); elements with row >= rmax or k >= kmax read as 0.
 // ---------------------------------------------------------------------------
 
 // K-contiguous operand: element (row, k) at base[row * ld + k]. Each thread
@@ -75,26 +126,28 @@ struct StageKC {
 
     __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld,
                                          int r0, int rmax, int k0, int kmax, int tid) {
+        const rsrc_t rs = make_rsrc(base + r0 * ld + k0);
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int item = p * NT + tid;
-            const int row = r0 + item / TPR;
-            const int k = k0 + (item % TPR) * 8;
-            const bool live = (ITEMS % NT == 0 || item < ITEMS) && row < rmax;
-            const float* src = base + (int64_t)row * ld + k;
+            const int dr = item / TPR;
+            const int dk = (item % TPR) * 8;
+            const bool live = (ITEMS % NT == 0 || item < ITEMS) && r0 + dr < rmax;
+            const uint32_t off = (uint32_t)(dr * ld + dk) * 4u;
             if constexpr (VEC == 4) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    floatx4 x = {0.f, 0.f, 0.f, 0.f};
-                    if (live && k + 4 * h < kmax)
-                        x = *reinterpret_cast<const floatx4*>(src + 4 * h);
+                    const bool ok = live && k0 + dk + 4 * h < kmax;
+                    const floatx4 x = buf_load4(rs, ok ? off + 16u * h : kBufOOB);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) v[p][4 * h + j] = x[j];
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    v[p][j] = (live && k + j < kmax) ? src[j] : 0.f;
+                for (int j = 0; j < 8; ++j) {
+                    const bool ok = live && k0 + dk + j < kmax;
+                    v[p][j] = buf_load1(rs, ok ? off + 4u * j : kBufOOB);
+                }
             }
         }
     }
@@ -124,25 +177,28 @@ struct StageMNC {
 
     __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld,
                                          int r0, int rmax, int k0, int kmax, int tid) {
+        const rsrc_t rs = make_rsrc(base + k0 * ld + r0);
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int item = p * NT + tid;
-            const int row = r0 + (item % CG) * 4;
-            const int k = k0 + (item / CG) * 8;
+            const int dr = (item % CG) * 4;
+            const int dk = (item / CG) * 8;
             const bool live = ITEMS % NT == 0 || item < ITEMS;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float* src = base + (int64_t)(k + j) * ld + row;
-                const bool kin = live && k + j < kmax;
+                const bool kin = live && k0 + dk + j < kmax;
+                const uint32_t off = (uint32_t)((dk + j) * ld + dr) * 4u;
                 if constexpr (VEC == 4) {
-                    floatx4 x = {0.f, 0.f, 0.f, 0.f};
-                    if (kin && row < rmax) x = *reinterpret_cast<const floatx4*>(src);
+                    const bool ok = kin && r0 + dr < rmax;
+                    const floatx4 x = buf_load4(rs, ok ? off : kBufOOB);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[p][j][q] = x[q];
                 } else {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        v[p][j][q] = (kin && row + q < rmax) ? src[q] : 0.f;
+                    for (int q = 0; q < 4; ++q) {
+                        const bool ok = kin && r0 + dr + q < rmax;
+                        v[p][j][q] = buf_load1(rs, ok ? off + 4u * q : kBufOOB);
+                    }
                 }
             }
         }
@@ -167,27 +223,45 @@ struct StageMNC {
     }
 };
 
+// Bytes a K-contiguous stager's resource must span for a ROWS x BK tile with
+// leading dimension ld (host-side check against kMaxTileSpanBytes).
+inline int64_t span_kc(int rows, int bk, int64_t ld) { return ((int64_t)rows * ld + bk) * 4; }
+inline int64_t span_mnc(int rows, int bk, int64_t ld) { return ((int64_t)bk * ld + rows) * 4; }
+
 // ---------------------------------------------------------------------------
 // Wave-level MFMA over one BK slice: the wave owns a (TM*32) x (TN*32) block of
-// the block tile at (wm0, wn0), accumulators acc[TM][TN].
+// the block tile at (wm0, wn0), accumulators acc[TM][TN]. The fragments of
+// k-step kk+1 are read from LDS while the matrix cores work on k-step kk.
 // Accumulator layout of v_mfma_f32_32x32x16_f16 (lane l, element r):
 //   row = 8*(r/4) + 4*(l/32) + r%4, col = l%32.
+// Operand layout: lane l holds row l%32, k = 8*(l/32) .. 8*(l/32)+7.
 // ---------------------------------------------------------------------------
+template <int BK, int TM, int TN>
+__device__ __forceinline__ void read_frags(const half_t* As, const half_t* Bs, int wm0, int wn0,
+                                           int lane, int kk, half8 (&a)[TM], half8 (&b)[TN]) {
+    const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = lds_read8<BK>(As, wm0 + i * 32 + (lane & 31), chunk);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j] = lds_read8<BK>(Bs, wn0 + j * 32 + (lane & 31), chunk);
+}
+
 template <int BK, int TM, int TN>
 __device__ __forceinline__ void mfma_slice(const half_t* As, const half_t* Bs, int wm0,
                                            int wn0, int lane, floatx16 (&acc)[TM][TN]) {
+    constexpr int KK = BK / 16;
+    half8 a[2][TM], b[2][TN];
+    read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, 0, a[0], b[0]);
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-        const int chunk = kk * 2 + (lane >> 5);
-        half8 a[TM], b[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = lds_read8<BK>(As, wm0 + i * 32 + (lane & 31), chunk);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = lds_read8<BK>(Bs, wn0 + j * 32 + (lane & 31), chunk);
+    for (int kk = 0; kk < KK; ++kk) {
+        if (kk + 1 < KK)
+            read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, kk + 1, a[(kk + 1) & 1],
+                                   b[(kk + 1) & 1]);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(a[i], b[j], acc[i][j]);
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = mfma32x32x16(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
     }
 }
 
