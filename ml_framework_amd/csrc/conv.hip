@@ -14,6 +14,7 @@
 //   wgrad    dW[f,c,r,s] = sum_{b,ho,wo} Y[b,f,ho,wo] X[b,c,ho*sh-ph+r,wo*sw-pw+s]
 //            = conv2d dW   (convolution.cu:268-366, 431-452)
 //            = convT dW    (upsampling.cu:202-301, 354-374; roles of X, dY swapped)
+#include "conv_band.h"
 #include "gather.h"
 #include "kernels.h"
 #include "plan.h"
@@ -239,6 +240,10 @@ int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int
     if (npix > 0x7fffffff || K > 0x7fffffff || (int64_t)B * C * H * W > (int64_t)1 << 40)
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
     if (npix == 0 || F == 0) return SEERA_OK;
+    bool used = false;
+    SEERA_TRY(band_conv_fwd(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used));
+    if (used) return SEERA_OK;
+    // Gather path: any width, any tile size.
     FwdGather g{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)npix};
     const Plan pl = plan_tiles(F, (int)npix, (int)K, true, false);
     const bool va = aligned16(Wt) && K % 4 == 0;
@@ -258,6 +263,11 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     if (npix > 0x7fffffff || K > 0x7fffffff)
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
     if (npix == 0 || C == 0) return SEERA_OK;
+    bool used = false;
+    SEERA_TRY(band_conv_dgrad(Yin, Wconv, out, B, F, Hi, Wi, C, H, W, R, S, sh, sw, ph, pw, st,
+                              &used));
+    if (used) return SEERA_OK;
+    // Gather path: any width, any stride.
     void* ws = nullptr;
     const int64_t wn = (int64_t)F * C * R * S;
     SEERA_TRY(workspace(sizeof(float) * (size_t)std::max<int64_t>(wn, 1), &ws));

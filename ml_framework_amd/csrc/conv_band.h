@@ -1,0 +1,58 @@
+// conv_band.h -- LDS-band convolution (conv_band.hip): argument block and
+// host entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "runtime.h"
+
+namespace seera {
+
+typedef _Float16 half_t;
+
+constexpr int kBandMaxPhases = 16;
+constexpr int64_t kBandMaxLds = 160 * 1024;
+
+// One stride phase of a launch: the output sub-grid it writes and how its
+// taps read the input (see conv_band.hip for the formula).
+struct BandPhase {
+    int Ho, Wo;      // phase output grid
+    int T, U;        // taps along rows / columns
+    int iph, ipw;    // input row = oh*ish + t - iph
+    int oph, opw;    // output row = oh*osh + oph
+    int64_t woff;    // offset (halves) of this phase's prepared weights
+    int nrb, ncb;    // row / column tiles of the phase grid
+    int block0;      // first blockIdx.x of the phase
+};
+
+struct BandConvArgs {
+    const float* in;     // [B, C, H, W] fp32
+    const half_t* wk;    // prepared fp16 weights
+    float* out;          // [B, F, Hout, Wout] fp32
+    int B, C, H, W;
+    int F, Hout, Wout;
+    int ish, isw, osh, osw;
+    int TH, WC;          // output tile rows / columns per block
+    int BR, BC4;         // input band rows / columns (BC4 % 4 == 0)
+    int max_taps;
+    int nchunks, nftiles, nblocks;
+    int64_t lds_bytes;
+    int nphase;
+    BandPhase ph[kBandMaxPhases];
+};
+
+// Forward convolution Y = conv(X, W) (W [F, C, R, S]) when the band path
+// applies (input width % 4 == 0, tile fits LDS); *used reports whether it ran.
+int band_conv_fwd(const float* X, const float* W, float* Y, int B, int C, int H, int W_in, int F,
+                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used);
+
+// Transposed convolution out[B, Cc, H, W] of Y [B, Fc, Hi, Wi] with the conv
+// weight W [Fc, Cc, R, S] (stride, pad of the forward conv), by stride phases.
+int band_conv_dgrad(const float* Y, const float* W, float* out, int B, int Fc, int Hi, int Wi,
+                    int Cc, int H, int W_out, int R, int S, int sh, int sw, int ph, int pw,
+                    hipStream_t st, bool* used);
+
+}  // namespace seera

@@ -1,0 +1,389 @@
+// conv_band.hip -- LDS-band implicit-GEMM convolution for gfx950.
+//
+// One kernel covers every convolution-shaped pass of the hot path whose input
+// rows are float4-aligned (W % 4 == 0):
+//   conv2d forward       (convolution.cu:15-101, 367-389)
+//   conv2d dX            (convolution.cu:144-265, 401-429)   flipped weights
+//   convT forward        (upsampling.cu:15-126, 376-401)     = conv2d dX
+//   convT dX             (upsampling.cu:128-197, 337-346)    = conv2d forward
+//
+// General form computed by one launch, per phase z (stride phases of the
+// transposed convolutions; a plain forward convolution has one phase):
+//   out[b, f, oh*osh + oph_z, ow*osw + opw_z] =
+//     sum_{c < Cin, t < T_z, u < U_z} Wk_z[f, t, u, c] *
+//                                     in[b, c, oh*ish + t - iph_z, ow*isw + u - ipw_z]
+// with zero outside the input. Wk_z is the prepared fp16 weight tensor.
+//
+// A block owns one image, a TH x WC tile of the phase's output grid and 64
+// output channels. For each chunk of 32 input channels it stages
+//   * the input band those outputs read (rows x cols x 32 channels, rounded
+//     to fp16, channel-last so that 8 channels of one pixel are 16 bytes), and
+//   * the 64 x taps x 32 weight slice
+// in LDS once; every tap then reads shifted 16-byte windows of the band as
+// the B operand of v_mfma_f32_16x16x32_f16 (32 channels of one tap per MFMA).
+// HBM sees each input element once per output-channel tile (plus the halo
+// rows of neighbouring bands, mostly served by L2) and each output once: the
+// im2col matrix is never formed.
+#include "conv_band.h"
+#include "mfma_core.h"
+
+namespace seera {
+namespace {
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Band layout: pixel p (row-major over the band's rows x BC4 columns) holds 32
+// channels = four 16-byte chunks. Two pixels share a 128-byte bank window; the
+// chunk order inside a pixel is rotated by (p >> 1) & 3, which makes any eight
+// consecutive pixels at one chunk hit eight distinct 16-byte slots (the MFMA B
+// reads of a stride-1 convolution). Stride-2 reads touch pixels of one parity
+// and see two-way conflicts.
+__device__ __forceinline__ int band_off(int p, int chunk) {
+    return p * 32 + ((chunk ^ ((p >> 1) & 3)) << 3);
+}
+
+constexpr int kNT = 256;  // threads per block (4 waves: 2 filter halves x 2 pixel halves)
+
+template <int PGW>
+__global__ __launch_bounds__(kNT) void band_conv_kernel(const BandConvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+
+    // Phase and tile of this block.
+    const int bx = blockIdx.x;
+    int z = 0;
+    while (z + 1 < a.nphase && bx >= a.ph[z + 1].block0) ++z;
+    const BandPhase& P = a.ph[z];
+    int local = bx - P.block0;
+    const int cb = local % P.ncb;
+    local /= P.ncb;
+    const int rb = local % P.nrb;
+    const int b = local / P.nrb;
+    const int oh0 = rb * a.TH, ow0 = cb * a.WC;
+    const int ftile = blockIdx.y;
+    const int taps = P.T * P.U;
+
+    half_t* const wl = smem;                         // taps x 64 f x 32 c
+    half_t* const bl = smem + a.max_taps * 2048;     // BR x BC4 pixels x 32 c
+
+    const int ir0 = oh0 * a.ish - P.iph;             // input row of band row 0
+    const int icr = ow0 * a.isw - P.ipw;             // input col of output col ow0, tap 0
+    const int ic0 = icr >= 0 ? (icr & ~3) : -((-icr + 3) & ~3);  // floor to a multiple of 4
+    const int coff = icr - ic0;                      // 0..3
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wf = wave & 1, wp = wave >> 1;
+    const int tile_px = a.TH * a.WC;
+
+    // Band pixel of each of this lane's output pixels at tap (0, 0).
+    int pbase[PGW];
+#pragma unroll
+    for (int i = 0; i < PGW; ++i) {
+        int px = (wp * PGW + i) * 16 + (lane & 15);
+        if (px >= tile_px) px = 0;  // padding lanes: computed, never stored
+        const int ohl = px / a.WC, owl = px - ohl * a.WC;
+        pbase[i] = ohl * a.ish * a.BC4 + owl * a.isw + coff;
+    }
+
+    floatx4_t acc[2][PGW];
+#pragma unroll
+    for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+        for (int i = 0; i < PGW; ++i) acc[fi][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t in_img = (int64_t)b * a.C * a.H * a.W;
+    const int nq = a.BC4 >> 2;                       // column quads per band row
+    const int band_items = a.BR * nq * 4;            // (row, quad, 8-channel group)
+    const half_t* wsrc_base = a.wk + P.woff + (int64_t)ftile * a.nchunks * taps * 2048;
+
+    for (int ch = 0; ch < a.nchunks; ++ch) {
+        __syncthreads();  // the previous chunk's MFMAs are done with the LDS tiles
+
+        // Weights: taps x 2048 halves, contiguous in Wk; 16-byte pieces.
+        const half_t* wsrc = wsrc_base + (int64_t)ch * taps * 2048;
+        for (int pc = tid; pc < taps * 256; pc += kNT) {
+            const half8 v = *reinterpret_cast<const half8*>(wsrc + pc * 8);
+            const int tap = pc >> 8, f = (pc >> 2) & 63, c8 = pc & 3;
+            lds_write8<32>(wl + tap * 2048, f, c8, v);
+        }
+
+        // Input band: each item is 4 consecutive columns x 8 channels, loaded
+        // as 8 float4 rows of the NCHW tensor and transposed into 4 pixels.
+        const int cbase = ch * 32;
+        for (int it = tid; it < band_items; it += kNT) {
+            const int cg = it & 3;
+            const int rq = it >> 2;
+            const int r = rq / nq, q4 = rq - r * nq;
+            const int hin = ir0 + r;
+            const int win = ic0 + q4 * 4;
+            const bool rowok = (unsigned)hin < (unsigned)a.H && (unsigned)win < (unsigned)a.W;
+            float v[8][4];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = cbase + cg * 8 + j;
+                floatx4 x = {0.f, 0.f, 0.f, 0.f};
+                if (rowok && c < a.C)
+                    x = *reinterpret_cast<const floatx4*>(a.in + in_img +
+                                                          ((int64_t)c * a.H + hin) * a.W + win);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[j][q] = x[q];
+            }
+            const int p0 = r * a.BC4 + q4 * 4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float col[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) col[j] = v[j][q];
+                *reinterpret_cast<half8*>(bl + band_off(p0 + q, cg)) = pack8(col);
+            }
+        }
+        __syncthreads();
+
+        // MFMAs over every tap of this channel chunk.
+        for (int t = 0; t < P.T; ++t) {
+            for (int u = 0; u < P.U; ++u) {
+                const int tap = t * P.U + u;
+                const int tapoff = t * a.BC4 + u;
+                half8 fa[2], fb[PGW];
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+                    fa[fi] = lds_read8<32>(wl + tap * 2048, (wf * 2 + fi) * 16 + (lane & 15),
+                                           lane >> 4);
+#pragma unroll
+                for (int i = 0; i < PGW; ++i)
+                    fb[i] = *reinterpret_cast<const half8*>(bl + band_off(pbase[i] + tapoff,
+                                                                          lane >> 4));
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                    for (int i = 0; i < PGW; ++i) acc[fi][i] = mfma16x16x32(fa[fi], fb[i], acc[fi][i]);
+            }
+        }
+    }
+
+    // Store: lane holds rows f = 4*(lane/16) + r of a 16x16 tile, column = pixel lane%16.
+#pragma unroll
+    for (int i = 0; i < PGW; ++i) {
+        const int px = (wp * PGW + i) * 16 + (lane & 15);
+        if (px >= tile_px) continue;
+        const int ohl = px / a.WC, owl = px - ohl * a.WC;
+        const int oh = oh0 + ohl, ow = ow0 + owl;
+        if (oh >= P.Ho || ow >= P.Wo) continue;
+        const int64_t opix = (int64_t)(oh * a.osh + P.oph) * a.Wout + ow * a.osw + P.opw;
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi) {
+            const int fb0 = ftile * 64 + (wf * 2 + fi) * 16 + 4 * (lane >> 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int f = fb0 + r;
+                if (f < a.F) a.out[((int64_t)b * a.F + f) * a.Hout * a.Wout + opix] = acc[fi][i][r];
+            }
+        }
+    }
+}
+
+// Wk[ftile][chunk][tap][f64][c32] for a forward convolution: W is [F, C, R, S].
+__global__ void prep_fwd_weights(const float* __restrict__ W, half_t* __restrict__ wk, int F, int C,
+                                 int R, int S, int nchunks, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int c32 = (int)(i & 31), f64 = (int)((i >> 5) & 63);
+    int64_t rest = i >> 11;
+    const int taps = R * S;
+    const int tap = (int)(rest % taps);
+    rest /= taps;
+    const int chunk = (int)(rest % nchunks);
+    const int ftile = (int)(rest / nchunks);
+    const int f = ftile * 64 + f64, c = chunk * 32 + c32;
+    const int t = tap / S, u = tap - t * S;
+    float v = 0.f;
+    if (f < F && c < C) v = W[(((int64_t)f * C + c) * R + t) * S + u];
+    wk[i] = to_half(v);
+}
+
+// Wk for one stride phase of the transposed convolution (conv dX): the
+// band kernel's output channel is the conv input channel c (< Cc), its input
+// channel is the conv output channel f (< Fc); tap (t, u) of the phase reads
+// W[f, c, r0h + sh*(T-1-t), r0w + sw*(U-1-u)] (W is [Fc, Cc, R, S]).
+__global__ void prep_dgrad_weights(const float* __restrict__ W, half_t* __restrict__ wk, int Fc,
+                                   int Cc, int R, int S, int sh, int sw, int r0h, int r0w, int T,
+                                   int U, int nchunks, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int k32 = (int)(i & 31), o64 = (int)((i >> 5) & 63);
+    int64_t rest = i >> 11;
+    const int taps = T * U;
+    const int tap = (int)(rest % taps);
+    rest /= taps;
+    const int chunk = (int)(rest % nchunks);
+    const int otile = (int)(rest / nchunks);
+    const int c = otile * 64 + o64;   // conv input channel = band output channel
+    const int f = chunk * 32 + k32;   // conv output channel = band input channel
+    const int t = tap / U, u = tap - t * U;
+    const int r = r0h + sh * (T - 1 - t), s = r0w + sw * (U - 1 - u);
+    float v = 0.f;
+    if (c < Cc && f < Fc) v = W[(((int64_t)f * Cc + c) * R + r) * S + s];
+    wk[i] = to_half(v);
+}
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Chooses the output tile (TH x WC, at most 224 pixels so that each wave owns
+// at most 7 pixel groups of 16) and checks the LDS budget.
+bool plan_tile(BandConvArgs& a) {
+    int max_ho = 0, max_wo = 0;
+    a.max_taps = 0;
+    for (int z = 0; z < a.nphase; ++z) {
+        max_ho = std::max(max_ho, a.ph[z].Ho);
+        max_wo = std::max(max_wo, a.ph[z].Wo);
+        a.max_taps = std::max(a.max_taps, a.ph[z].T * a.ph[z].U);
+    }
+    if (max_ho == 0 || max_wo == 0) return true;
+    int max_t = 0, max_u = 0;
+    for (int z = 0; z < a.nphase; ++z) {
+        max_t = std::max(max_t, a.ph[z].T);
+        max_u = std::max(max_u, a.ph[z].U);
+    }
+    a.WC = std::min(max_wo, 224);
+    for (a.TH = std::max(1, std::min(max_ho, 224 / a.WC)); a.TH >= 1; --a.TH) {
+        a.BR = (a.TH - 1) * a.ish + std::max(max_t, 1);
+        a.BC4 = ((a.WC - 1) * a.isw + std::max(max_u, 1) + 3 + 3) & ~3;
+        a.lds_bytes = (int64_t)a.max_taps * 2048 * 2 + (int64_t)a.BR * a.BC4 * 64;
+        if (a.lds_bytes <= kBandMaxLds) break;
+    }
+    if (a.TH < 1) return false;
+    for (int z = 0, blocks = 0; z < a.nphase; ++z) {
+        BandPhase& p = a.ph[z];
+        p.nrb = ceil_div(p.Ho, a.TH);
+        p.ncb = ceil_div(p.Wo, a.WC);
+        p.block0 = blocks;
+        blocks += a.B * p.nrb * p.ncb;
+        a.nblocks = blocks;
+    }
+    return true;
+}
+
+template <int PGW>
+hipError_t launch_pgw(const BandConvArgs& a, hipStream_t st) {
+    auto kern = band_conv_kernel<PGW>;
+    if (a.lds_bytes > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)a.lds_bytes);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, dim3(a.nblocks, a.nftiles), dim3(kNT), (size_t)a.lds_bytes, st, a);
+    return hipGetLastError();
+}
+
+int launch_band(const BandConvArgs& a, hipStream_t st) {
+    if (a.nblocks == 0 || a.nftiles == 0) return SEERA_OK;
+    const int pgw = ceil_div(ceil_div(a.TH * a.WC, 16), 2);
+    hipError_t e;
+    switch (pgw) {
+        case 1: e = launch_pgw<1>(a, st); break;
+        case 2: e = launch_pgw<2>(a, st); break;
+        case 3: e = launch_pgw<3>(a, st); break;
+        case 4: e = launch_pgw<4>(a, st); break;
+        case 5: e = launch_pgw<5>(a, st); break;
+        case 6: e = launch_pgw<6>(a, st); break;
+        default: e = launch_pgw<7>(a, st); break;
+    }
+    if (e != hipSuccess) return fail_hip(e, "band conv launch");
+    return SEERA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F,
+                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used) {
+    *used = false;
+    if (W % 4 != 0 || !aligned16(X)) return SEERA_OK;
+    BandConvArgs a{};
+    a.in = X;
+    a.out = Y;
+    a.B = B; a.C = C; a.H = H; a.W = W;
+    a.F = F;
+    a.Hout = (H + 2 * ph - R) / sh + 1;
+    a.Wout = (W + 2 * pw - S) / sw + 1;
+    a.ish = sh; a.isw = sw; a.osh = 1; a.osw = 1;
+    a.nphase = 1;
+    a.ph[0] = BandPhase{a.Hout, a.Wout, R, S, ph, pw, 0, 0, 0, 0, 0, 0};
+    a.nchunks = ceil_div(C, 32);
+    a.nftiles = ceil_div(F, 64);
+    if (!plan_tile(a)) return SEERA_OK;
+    const int64_t wsz = (int64_t)a.nftiles * a.nchunks * R * S * 2048;
+    void* ws = nullptr;
+    SEERA_TRY(workspace(sizeof(half_t) * (size_t)wsz, &ws));
+    a.wk = static_cast<const half_t*>(ws);
+    hipLaunchKernelGGL(prep_fwd_weights, dim3((unsigned)((wsz + 255) / 256)), dim3(256), 0, st, Wt,
+                       static_cast<half_t*>(ws), F, C, R, S, a.nchunks, wsz);
+    SEERA_HIP_TRY(hipGetLastError());
+    SEERA_TRY(launch_band(a, st));
+    *used = true;
+    return SEERA_OK;
+}
+
+int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int Fc, int Hi, int Wi,
+                    int Cc, int H, int W, int R, int S, int sh, int sw, int ph, int pw,
+                    hipStream_t st, bool* used) {
+    *used = false;
+    if (Wi % 4 != 0 || !aligned16(Yin) || sh * sw > kBandMaxPhases) return SEERA_OK;
+    BandConvArgs a{};
+    a.in = Yin;
+    a.out = out;
+    a.B = B; a.C = Fc; a.H = Hi; a.W = Wi;
+    a.F = Cc; a.Hout = H; a.Wout = W;
+    a.ish = 1; a.isw = 1; a.osh = sh; a.osw = sw;
+    a.nchunks = ceil_div(Fc, 32);
+    a.nftiles = ceil_div(Cc, 64);
+    struct Axis { int r0, T, q, n; };
+    auto axis = [](int phi, int p, int s, int K, int out_len) {
+        Axis x;
+        x.r0 = (phi + p) % s;
+        x.T = K > x.r0 ? (K - x.r0 + s - 1) / s : 0;
+        x.q = (phi + p - x.r0) / s;
+        x.n = out_len > phi ? (out_len - phi + s - 1) / s : 0;
+        return x;
+    };
+    int64_t woff = 0;
+    int zi = 0;
+    Axis ax[kBandMaxPhases][2];
+    for (int phh = 0; phh < sh; ++phh)
+        for (int phw = 0; phw < sw; ++phw, ++zi) {
+            const Axis xh = axis(phh, ph, sh, R, H), xw = axis(phw, pw, sw, S, W);
+            ax[zi][0] = xh;
+            ax[zi][1] = xw;
+            BandPhase& p = a.ph[zi];
+            p.Ho = xh.n; p.Wo = xw.n;
+            p.T = xh.T; p.U = xw.T;
+            p.iph = xh.T - 1 - xh.q;
+            p.ipw = xw.T - 1 - xw.q;
+            p.oph = phh; p.opw = phw;
+            p.woff = woff;
+            woff += (int64_t)a.nftiles * a.nchunks * xh.T * xw.T * 2048;
+        }
+    a.nphase = zi;
+    if (!plan_tile(a)) return SEERA_OK;
+    void* ws = nullptr;
+    SEERA_TRY(workspace(sizeof(half_t) * (size_t)std::max<int64_t>(woff, 1), &ws));
+    a.wk = static_cast<const half_t*>(ws);
+    for (int z = 0; z < a.nphase; ++z) {
+        const int64_t n = (int64_t)a.nftiles * a.nchunks * a.ph[z].T * a.ph[z].U * 2048;
+        if (n == 0) continue;
+        hipLaunchKernelGGL(prep_dgrad_weights, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           Wconv, static_cast<half_t*>(ws) + a.ph[z].woff, Fc, Cc, R, S, sh, sw,
+                           ax[z][0].r0, ax[z][1].r0, a.ph[z].T, a.ph[z].U, a.nchunks, n);
+        SEERA_HIP_TRY(hipGetLastError());
+    }
+    SEERA_TRY(launch_band(a, st));
+    *used = true;
+    return SEERA_OK;
+}
+
+}  // namespace seera
