@@ -309,6 +309,10 @@ int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, i
         SEERA_HIP_TRY(hipMemsetAsync(dW, 0, sizeof(float) * (size_t)F * crs, st));
         return SEERA_OK;
     }
+    bool used = false;
+    SEERA_TRY(band_conv_wgrad(Y, X, dW, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used));
+    if (used) return SEERA_OK;
+    // Gather path: any width, any kernel size.
     // Gathers only: the 64x64 tile, split over pixels.
     const Plan pl = plan_tiles(F, (int)crs, (int)npix, false, true);
     return run_plan<false>(p, pl, st);

@@ -56,3 +56,28 @@ int band_conv_dgrad(const float* Y, const float* W, float* out, int B, int Fc, i
                     hipStream_t st, bool* used);
 
 }  // namespace seera
+
+namespace seera {
+
+// Weight-gradient band kernel arguments (conv_band.hip).
+struct WgradArgs {
+    const float* dy;    // [B, F, Ho, Wo]
+    const float* x;     // [B, C, H, W]
+    float* part;        // [tiles][nsplit][64][CT*R*S] partial sums
+    int B, C, H, W, F, Ho, Wo, R, S, sh, sw, ph, pw;
+    int TH, WC8, BR;    // output tile (TH rows x WC8 columns, WC8 % 8 == 0), X rows per band
+    int KS;             // 32-pixel k-steps per tile
+    int nrb, ncb, items, ips, nsplit;
+    int nftile, nctile, CT;
+    int dy_stride;      // halves per filter row of the dY tile
+    int x_plane;        // halves per (s, channel) plane of the shifted X copies
+    int NL;             // float4 loads per 8-column X octet
+    int64_t lds_bytes;
+};
+
+// dW [F, C, R, S] = sum over (b, oh, ow) of dY[b, f, oh, ow] *
+// X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies.
+int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
+                    int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used);
+
+}  // namespace seera

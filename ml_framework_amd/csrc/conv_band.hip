@@ -296,6 +296,224 @@ int launch_band(const BandConvArgs& a, hipStream_t st) {
     return SEERA_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// Weight gradient (convolution.cu:268-366, 431-452; upsampling.cu:202-301):
+//   dW[f, c, r, s] = sum_{b, oh, ow} dY[b, f, oh, ow] * X[b, c, oh*sh - ph + r, ow*sw - pw + s]
+// a GEMM with M = filters, N = (tap, channel), K = output pixels. A block owns
+// 64 filters x CT channels x all taps and walks `ips` output tiles (TH x WC8
+// pixels of one image), accumulating in registers. Per tile it stages the
+// dY tile [64 f][pixels] and, per 32-channel chunk, S column-shifted fp16
+// copies of the X band: copy s holds X[c, row, ow*sw - pw + s] at column ow,
+// so every tap's B fragment (8 consecutive pixels of one channel) is one
+// aligned 16-byte LDS read. Row strides are 16 bytes past a multiple of
+// 128 bytes, so the 16 lanes of a fragment read (16 filters or 16 channels
+// at one pixel chunk) hit distinct banks. Each block writes its partial sum;
+// wgrad_reduce adds the partials in a fixed order.
+// ---------------------------------------------------------------------------
+
+// v[j] = w[O + j*SW] (0 past the window).
+template <int O, int SW, int NW>
+__device__ __forceinline__ void pick_at(const float (&w)[NW], float (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (O + j * SW < NW) ? w[O + j * SW] : 0.f;
+}
+
+// Same with a wave-uniform offset o in [0, 9].
+template <int SW, int NW>
+__device__ __forceinline__ void pick8(const float (&w)[NW], int o, float (&v)[8]) {
+    switch (o) {
+        case 0: pick_at<0, SW>(w, v); break;
+        case 1: pick_at<1, SW>(w, v); break;
+        case 2: pick_at<2, SW>(w, v); break;
+        case 3: pick_at<3, SW>(w, v); break;
+        case 4: pick_at<4, SW>(w, v); break;
+        case 5: pick_at<5, SW>(w, v); break;
+        case 6: pick_at<6, SW>(w, v); break;
+        case 7: pick_at<7, SW>(w, v); break;
+        case 8: pick_at<8, SW>(w, v); break;
+        default: pick_at<9, SW>(w, v); break;
+    }
+}
+
+constexpr int kWgNL = 6;  // float4 loads per X octet at most (S <= 7, stride <= 2)
+
+template <int NGW, int SW>
+__global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    half_t* const dyl = smem;                      // 64 x dy_stride
+    half_t* const xl = smem + 64 * a.dy_stride;    // S x 32 x x_plane
+
+    const int split = blockIdx.x, ty = blockIdx.y;
+    const int ftile = ty / a.nctile, ctile = ty - ftile * a.nctile;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NG = a.CT * a.R * a.S / 16;
+    const int cgroups = a.CT / 16;
+    const int noct = a.WC8 >> 3;
+
+    floatx4_t acc[4][NGW];
+#pragma unroll
+    for (int fg = 0; fg < 4; ++fg)
+#pragma unroll
+        for (int i = 0; i < NGW; ++i) acc[fg][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int it0 = split * a.ips, it1 = min(a.items, it0 + a.ips);
+    for (int item = it0; item < it1; ++item) {
+        int rem = item;
+        const int cb = rem % a.ncb;
+        rem /= a.ncb;
+        const int rb = rem % a.nrb;
+        const int b = rem / a.nrb;
+        const int oh0 = rb * a.TH, ow0 = cb * a.WC8;
+        const int valid_cols = a.Wo - ow0;
+
+        __syncthreads();  // previous tile's MFMAs are done with LDS
+        // dY tile: 64 filters x TH rows x WC8 columns, 8 columns per item.
+        const int dy_items = 64 * a.TH * noct;
+        for (int it = tid; it < dy_items; it += kNT) {
+            const int m = it % noct;
+            const int rest = it / noct;
+            const int ohl = rest % a.TH, fl = rest / a.TH;
+            const int f = ftile * 64 + fl, oh = oh0 + ohl, ow = ow0 + 8 * m;
+            float v[8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
+                if (f < a.F && oh < a.Ho && ow + 4 * h < a.Wo)
+                    x4 = *reinterpret_cast<const floatx4*>(
+                        a.dy + (((int64_t)b * a.F + f) * a.Ho + oh) * a.Wo + ow + 4 * h);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[4 * h + j] = x4[j];
+            }
+            *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) = pack8(v);
+        }
+
+        const int ir0 = oh0 * a.sh - a.ph;
+        const int xc0 = ow0 * a.sw - a.pw;                     // X column of (ow0, s = 0)
+        const int xb = xc0 >= 0 ? (xc0 & ~3) : -((-xc0 + 3) & ~3);
+        const int nchunk = a.CT / 32;
+        for (int ch = 0; ch < nchunk; ++ch) {
+            if (ch > 0) __syncthreads();
+            // Shifted X copies for channels [cbase, cbase + 32).
+            const int cbase = ctile * a.CT + ch * 32;
+            const int x_items = 32 * a.BR * noct;
+            for (int it = tid; it < x_items; it += kNT) {
+                const int m = it % noct;
+                const int rest = it / noct;
+                const int row = rest % a.BR, cl = rest / a.BR;
+                const int c = cbase + cl, hin = ir0 + row;
+                const int a0 = xb + 8 * m * SW;
+                float w[4 * kWgNL];
+                const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;
+                const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;
+#pragma unroll
+                for (int q = 0; q < kWgNL; ++q) {
+                    floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
+                    const int col = a0 + 4 * q;
+                    if (q < a.NL && rowok && (unsigned)col < (unsigned)a.W)
+                        x4 = *reinterpret_cast<const floatx4*>(src + col);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[4 * q + j] = x4[j];
+                }
+                for (int s = 0; s < a.S; ++s) {
+                    float v[8];
+                    pick8<SW>(w, xc0 - xb + s, v);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (8 * m + j >= valid_cols) v[j] = 0.f;  // columns past the output
+                    *reinterpret_cast<half8*>(xl + (s * 32 + cl) * a.x_plane + row * a.WC8 + 8 * m) =
+                        pack8(v);
+                }
+            }
+            __syncthreads();
+
+            for (int ks = 0; ks < a.KS; ++ks) {
+                const int px0 = ks * 32 + 8 * (lane >> 4);
+                const int ohl = px0 / a.WC8, owl = px0 - ohl * a.WC8;
+                half8 fa[4];
+#pragma unroll
+                for (int fg = 0; fg < 4; ++fg)
+                    fa[fg] = *reinterpret_cast<const half8*>(dyl + (fg * 16 + (lane & 15)) * a.dy_stride +
+                                                             px0);
+#pragma unroll
+                for (int i = 0; i < NGW; ++i) {
+                    const int g = wave * NGW + i;
+                    if (g >= NG) continue;
+                    const int tap = g / cgroups, cq = g - tap * cgroups;
+                    if ((cq >> 1) != ch) continue;
+                    const int cl = (cq & 1) * 16 + (lane & 15);
+                    const int r = tap / a.S, s = tap - r * a.S;
+                    const half8 fb = *reinterpret_cast<const half8*>(
+                        xl + (s * 32 + cl) * a.x_plane + (ohl * a.sh + r) * a.WC8 + owl);
+#pragma unroll
+                    for (int fg = 0; fg < 4; ++fg) acc[fg][i] = mfma16x16x32(fa[fg], fb, acc[fg][i]);
+                }
+            }
+        }
+    }
+
+    // Partial sums: part[ty][split][f64][n], n = tap * CT + channel within the tile.
+    const int ntot = a.CT * a.R * a.S;
+    float* const dst = a.part + ((int64_t)ty * a.nsplit + split) * 64 * ntot;
+#pragma unroll
+    for (int i = 0; i < NGW; ++i) {
+        const int g = wave * NGW + i;
+        if (g >= NG) continue;
+        const int n = g * 16 + (lane & 15);
+#pragma unroll
+        for (int fg = 0; fg < 4; ++fg)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[(int64_t)(fg * 16 + 4 * (lane >> 4) + r) * ntot + n] = acc[fg][i][r];
+    }
+}
+
+// dW[f, c, r, s] = sum over splits (in order) of the partials.
+__global__ void wgrad_reduce(const float* __restrict__ part, float* __restrict__ dW, int F, int C,
+                             int R, int S, int CT, int nctile, int nsplit) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)F * C * R * S;
+    if (i >= total) return;
+    const int s = (int)(i % S), r = (int)((i / S) % R);
+    const int c = (int)((i / ((int64_t)R * S)) % C), f = (int)(i / ((int64_t)C * R * S));
+    const int ty = (f / 64) * nctile + c / CT;
+    const int ntot = CT * R * S;
+    const int n = (r * S + s) * CT + c % CT;
+    const float* p = part + ((int64_t)ty * nsplit * 64 + (f % 64)) * ntot + n;
+    float acc = 0.f;
+    for (int z = 0; z < nsplit; ++z) acc += p[(int64_t)z * 64 * ntot];
+    dW[i] = acc;
+}
+
+template <int SW>
+hipError_t launch_wgrad_sw(const WgradArgs& a, int ngw, hipStream_t st) {
+    const void* k = nullptr;
+    switch (ngw) {
+        case 1: k = reinterpret_cast<const void*>(band_wgrad_kernel<1, SW>); break;
+        case 2: k = reinterpret_cast<const void*>(band_wgrad_kernel<2, SW>); break;
+        case 3: k = reinterpret_cast<const void*>(band_wgrad_kernel<3, SW>); break;
+        case 4: k = reinterpret_cast<const void*>(band_wgrad_kernel<4, SW>); break;
+        case 5: k = reinterpret_cast<const void*>(band_wgrad_kernel<5, SW>); break;
+        case 6: k = reinterpret_cast<const void*>(band_wgrad_kernel<6, SW>); break;
+        case 7: k = reinterpret_cast<const void*>(band_wgrad_kernel<7, SW>); break;
+        case 8: k = reinterpret_cast<const void*>(band_wgrad_kernel<8, SW>); break;
+        default: k = reinterpret_cast<const void*>(band_wgrad_kernel<9, SW>); break;
+    }
+    if (a.lds_bytes > 65536) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)a.lds_bytes);
+        if (e != hipSuccess) return e;
+    }
+    void* args[] = {const_cast<WgradArgs*>(&a)};
+    return hipLaunchKernel(k, dim3(a.nsplit, a.nftile * a.nctile), dim3(kNT), args,
+                           (size_t)a.lds_bytes, st);
+}
+
+// Smallest stride >= n halves that is 16 bytes past a multiple of 128 bytes.
+int stride16(int n) {
+    n = (n + 7) & ~7;
+    return n + ((8 - n % 64) + 64) % 64;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -382,6 +600,59 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
         SEERA_HIP_TRY(hipGetLastError());
     }
     SEERA_TRY(launch_band(a, st));
+    *used = true;
+    return SEERA_OK;
+}
+
+
+int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
+                    int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used) {
+    *used = false;
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    if (Wo % 4 != 0 || W % 4 != 0 || sw > 2 || S > 7 || R * S > 18 || !aligned16(Y) ||
+        !aligned16(X) || B == 0)
+        return SEERA_OK;
+    WgradArgs a{};
+    a.dy = Y; a.x = X;
+    a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Ho = Ho; a.Wo = Wo;
+    a.R = R; a.S = S; a.sh = sh; a.sw = sw; a.ph = ph; a.pw = pw;
+    a.CT = (R * S <= 9 && C > 32) ? 64 : 32;
+    a.nftile = ceil_div(F, 64);
+    a.nctile = ceil_div(C, a.CT);
+    a.NL = (3 + S - 1 + 7 * sw + 1 + 3) / 4;
+    a.WC8 = (std::min(Wo, 224) + 7) & ~7;
+    a.ncb = ceil_div(Wo, a.WC8);
+    // Rows per tile: about 224 pixels, TH * WC8 a multiple of 32.
+    const int th_mult = a.WC8 % 32 == 0 ? 1 : a.WC8 % 16 == 0 ? 2 : 4;
+    int th = std::max(1, std::min(Ho, 224 / a.WC8));
+    th = (th + th_mult - 1) / th_mult * th_mult;
+    for (;; th -= th_mult) {
+        if (th < th_mult) return SEERA_OK;
+        a.TH = th;
+        a.BR = (th - 1) * sh + R;
+        a.dy_stride = stride16(th * a.WC8);
+        a.x_plane = stride16(a.BR * a.WC8);
+        a.lds_bytes = 2 * ((int64_t)64 * a.dy_stride + (int64_t)S * 32 * a.x_plane);
+        if (a.lds_bytes <= kBandMaxLds) break;
+    }
+    a.KS = a.TH * a.WC8 / 32;
+    a.nrb = ceil_div(Ho, a.TH);
+    a.items = B * a.nrb * a.ncb;
+    const int tiles = a.nftile * a.nctile;
+    int nsplit = std::max(1, std::min(a.items, ceil_div(256, tiles)));
+    a.ips = ceil_div(a.items, nsplit);
+    a.nsplit = ceil_div(a.items, a.ips);
+    const int ntot = a.CT * R * S;
+    const int ngw = ceil_div(ntot / 16, 4);
+    void* ws = nullptr;
+    SEERA_TRY(workspace(sizeof(float) * (size_t)tiles * a.nsplit * 64 * ntot, &ws));
+    a.part = static_cast<float*>(ws);
+    hipError_t e = sw == 1 ? launch_wgrad_sw<1>(a, ngw, st) : launch_wgrad_sw<2>(a, ngw, st);
+    if (e != hipSuccess) return fail_hip(e, "band wgrad launch");
+    const int64_t total = (int64_t)F * C * R * S;
+    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       a.part, dW, F, C, R, S, a.CT, a.nctile, a.nsplit);
+    SEERA_HIP_TRY(hipGetLastError());
     *used = true;
     return SEERA_OK;
 }
