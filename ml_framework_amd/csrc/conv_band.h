@@ -71,7 +71,6 @@ struct WgradArgs {
     int nftile, nctile, CT;
     int dy_stride;      // halves per filter row of the dY tile
     int x_plane;        // halves per (s, channel) plane of the shifted X copies
-    int NL;             // float4 loads per 8-column X octet
     int64_t lds_bytes;
 };
 

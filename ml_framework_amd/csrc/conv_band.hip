@@ -47,6 +47,7 @@ __device__ __forceinline__ int band_off(int p, int chunk) {
 }
 
 constexpr int kNT = 256;  // threads per block (4 waves: 2 filter halves x 2 pixel halves)
+constexpr int kBandMaxTaps = 16;  // taps per phase the band kernel handles (weights in LDS)
 
 template <int PGW>
 __global__ __launch_bounds__(kNT) void band_conv_kernel(const BandConvArgs a) {
@@ -102,12 +103,18 @@ __global__ __launch_bounds__(kNT) void band_conv_kernel(const BandConvArgs a) {
     for (int ch = 0; ch < a.nchunks; ++ch) {
         __syncthreads();  // the previous chunk's MFMAs are done with the LDS tiles
 
-        // Weights: taps x 2048 halves, contiguous in Wk; 16-byte pieces.
+        // Weights: taps x 2048 halves, contiguous in Wk; 16-byte pieces, one
+        // per tap for each thread (taps <= kBandMaxTaps), all loads issued
+        // before the LDS writes.
         const half_t* wsrc = wsrc_base + (int64_t)ch * taps * 2048;
-        for (int pc = tid; pc < taps * 256; pc += kNT) {
-            const half8 v = *reinterpret_cast<const half8*>(wsrc + pc * 8);
-            const int tap = pc >> 8, f = (pc >> 2) & 63, c8 = pc & 3;
-            lds_write8<32>(wl + tap * 2048, f, c8, v);
+        {
+            half8 wv[kBandMaxTaps];
+#pragma unroll
+            for (int tp = 0; tp < kBandMaxTaps; ++tp)
+                if (tp < taps) wv[tp] = *reinterpret_cast<const half8*>(wsrc + (tp * 256 + tid) * 8);
+#pragma unroll
+            for (int tp = 0; tp < kBandMaxTaps; ++tp)
+                if (tp < taps) lds_write8<32>(wl + tp * 2048, tid >> 2, tid & 3, wv[tp]);
         }
 
         // Input band: each item is 4 consecutive columns x 8 channels, loaded
@@ -241,6 +248,7 @@ bool plan_tile(BandConvArgs& a) {
         max_wo = std::max(max_wo, a.ph[z].Wo);
         a.max_taps = std::max(a.max_taps, a.ph[z].T * a.ph[z].U);
     }
+    if (a.max_taps > kBandMaxTaps) return false;
     if (max_ho == 0 || max_wo == 0) return true;
     int max_t = 0, max_u = 0;
     for (int z = 0; z < a.nphase; ++z) {
@@ -312,31 +320,61 @@ int launch_band(const BandConvArgs& a, hipStream_t st) {
 // wgrad_reduce adds the partials in a fixed order.
 // ---------------------------------------------------------------------------
 
-// v[j] = w[O + j*SW] (0 past the window).
-template <int O, int SW, int NW>
-__device__ __forceinline__ void pick_at(const float (&w)[NW], float (&v)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (O + j * SW < NW) ? w[O + j * SW] : 0.f;
-}
+// The loaded columns of one X item, held as one vector value (never an
+// addressable array, so it stays in registers).
+typedef float floatx44 __attribute__((ext_vector_type(44)));
 
-// Same with a wave-uniform offset o in [0, 9].
-template <int SW, int NW>
-__device__ __forceinline__ void pick8(const float (&w)[NW], int o, float (&v)[8]) {
-    switch (o) {
-        case 0: pick_at<0, SW>(w, v); break;
-        case 1: pick_at<1, SW>(w, v); break;
-        case 2: pick_at<2, SW>(w, v); break;
-        case 3: pick_at<3, SW>(w, v); break;
-        case 4: pick_at<4, SW>(w, v); break;
-        case 5: pick_at<5, SW>(w, v); break;
-        case 6: pick_at<6, SW>(w, v); break;
-        case 7: pick_at<7, SW>(w, v); break;
-        case 8: pick_at<8, SW>(w, v); break;
-        default: pick_at<9, SW>(w, v); break;
+// v[j] = element O + j*SW of the window (0 past its end); compile-time indices.
+template <int O, int SW>
+__device__ __forceinline__ void pick_at(const floatx44& w, float (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int e = O + j * SW;
+        v[j] = e < 44 ? w[e] : 0.f;
     }
 }
 
-constexpr int kWgNL = 6;  // float4 loads per X octet at most (S <= 7, stride <= 2)
+// Writes octets OC.. of one X item into shifted copy O - (band alignment):
+// octet m = grp*OCT + OC holds w[O + 8*OC*SW + j*SW], zeroed past the output.
+template <int O, int OC, int SW, int OCT>
+__device__ __forceinline__ void write_octets(const floatx44& w, int grp, int noct,
+                                             int valid_cols, half_t* dst) {
+    if constexpr (OC < OCT) {
+        const int m = grp * OCT + OC;
+        float v[8];
+        pick_at<O + 8 * OC * SW, SW>(w, v);
+        if (8 * m + 8 > valid_cols) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (8 * m + j >= valid_cols) v[j] = 0.f;
+        }
+        if (m < noct) *reinterpret_cast<half8*>(dst + 8 * m) = pack8(v);
+        write_octets<O, OC + 1, SW, OCT>(w, grp, noct, valid_cols, dst);
+    }
+}
+
+// Writes the S (<= 7) tap-shifted copies of one X item; OFF is the band's
+// column alignment (0..3), so every register index is a compile-time constant.
+template <int OFF, int SI, int SW, int OCT>
+__device__ __forceinline__ void write_shifts(const floatx44& w, int S, int grp, int noct,
+                                             int valid_cols, half_t* dst, int plane) {
+    if constexpr (SI < 7) {
+        if (SI < S) {
+            write_octets<OFF + SI, 0, SW, OCT>(w, grp, noct, valid_cols, dst + SI * plane);
+            write_shifts<OFF, SI + 1, SW, OCT>(w, S, grp, noct, valid_cols, dst, plane);
+        }
+    }
+}
+
+constexpr int kDyBatch = 4;  // dY items (2 float4 each) in flight per thread
+
+// X item = kXOct 8-column octets of one channel row; the float4 loads cover
+// the octets' columns for every tap shift (offset <= 3 + S - 1 <= 9, S <= 7).
+template <int SW>
+struct XItem {
+    static constexpr int OCT = SW == 1 ? 4 : 2;
+    static constexpr int F4 = (9 + (8 * OCT - 1) * SW + 1 + 3) / 4;
+};
 
 template <int NGW, int SW>
 __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
@@ -357,6 +395,18 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
 #pragma unroll
         for (int i = 0; i < NGW; ++i) acc[fg][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
+    // Per n-group of this wave: LDS offset of this lane's B fragment at pixel
+    // (0, 0) and the 32-channel chunk the group belongs to (-1: no group).
+    int boff[NGW], bchunk[NGW];
+#pragma unroll
+    for (int i = 0; i < NGW; ++i) {
+        const int g = wave * NGW + i;
+        const int tap = g / cgroups, cq = g - tap * cgroups;
+        const int r = tap / a.S, sh_ = tap - r * a.S;
+        bchunk[i] = g < NG ? (cq >> 1) : -1;
+        boff[i] = (sh_ * 32 + (cq & 1) * 16 + (lane & 15)) * a.x_plane + r * a.WC8;
+    }
+
     const int it0 = split * a.ips, it1 = min(a.items, it0 + a.ips);
     for (int item = it0; item < it1; ++item) {
         int rem = item;
@@ -368,24 +418,43 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
         const int valid_cols = a.Wo - ow0;
 
         __syncthreads();  // previous tile's MFMAs are done with LDS
-        // dY tile: 64 filters x TH rows x WC8 columns, 8 columns per item.
+        // dY tile: 64 filters x TH rows x WC8 columns, 8 columns per item. Each
+        // thread issues the loads of kDyBatch items before converting any, so
+        // that many loads are in flight.
         const int dy_items = 64 * a.TH * noct;
-        for (int it = tid; it < dy_items; it += kNT) {
-            const int m = it % noct;
-            const int rest = it / noct;
-            const int ohl = rest % a.TH, fl = rest / a.TH;
-            const int f = ftile * 64 + fl, oh = oh0 + ohl, ow = ow0 + 8 * m;
-            float v[8];
+        for (int it0 = tid; it0 < dy_items; it0 += kNT * kDyBatch) {
+            floatx4 v[kDyBatch][2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
-                if (f < a.F && oh < a.Ho && ow + 4 * h < a.Wo)
-                    x4 = *reinterpret_cast<const floatx4*>(
-                        a.dy + (((int64_t)b * a.F + f) * a.Ho + oh) * a.Wo + ow + 4 * h);
+            for (int k = 0; k < kDyBatch; ++k) {
+                const int it = it0 + k * kNT;
+                const int m = it % noct;
+                const int rest = it / noct;
+                const int ohl = rest % a.TH, fl = rest / a.TH;
+                const int f = ftile * 64 + fl, oh = oh0 + ohl, ow = ow0 + 8 * m;
+                const float* src = a.dy + (((int64_t)b * a.F + f) * a.Ho + oh) * a.Wo + ow;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) v[4 * h + j] = x4[j];
+                for (int h = 0; h < 2; ++h) {
+                    v[k][h] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    if (it < dy_items && f < a.F && oh < a.Ho && ow + 4 * h < a.Wo)
+                        v[k][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
+                }
             }
-            *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) = pack8(v);
+#pragma unroll
+            for (int k = 0; k < kDyBatch; ++k) {
+                const int it = it0 + k * kNT;
+                const int m = it % noct;
+                const int rest = it / noct;
+                const int ohl = rest % a.TH, fl = rest / a.TH;
+                float f8[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f8[j] = v[k][0][j];
+                    f8[4 + j] = v[k][1][j];
+                }
+                if (it < dy_items)
+                    *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) =
+                        pack8(f8);
+            }
         }
 
         const int ir0 = oh0 * a.sh - a.ph;
@@ -394,35 +463,39 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
         const int nchunk = a.CT / 32;
         for (int ch = 0; ch < nchunk; ++ch) {
             if (ch > 0) __syncthreads();
-            // Shifted X copies for channels [cbase, cbase + 32).
+            // Shifted X copies for channels [cbase, cbase + 32). An item is
+            // XItem::OCT octets of one channel row: its XItem::F4 float4 loads
+            // are all issued before any copy is written.
+            using XI = XItem<SW>;
             const int cbase = ctile * a.CT + ch * 32;
-            const int x_items = 32 * a.BR * noct;
+            const int ngrp = (noct + XI::OCT - 1) / XI::OCT;
+            const int x_items = 32 * a.BR * ngrp;
             for (int it = tid; it < x_items; it += kNT) {
-                const int m = it % noct;
-                const int rest = it / noct;
+                const int grp = it % ngrp;
+                const int rest = it / ngrp;
                 const int row = rest % a.BR, cl = rest / a.BR;
                 const int c = cbase + cl, hin = ir0 + row;
-                const int a0 = xb + 8 * m * SW;
-                float w[4 * kWgNL];
+                const int a0 = xb + 8 * XI::OCT * grp * SW;
                 const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;
                 const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;
+                static_assert(XI::F4 <= 11, "window exceeds 44 floats");
+                floatx44 w;
 #pragma unroll
-                for (int q = 0; q < kWgNL; ++q) {
-                    floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
+                for (int q = 0; q < 11; ++q) {
                     const int col = a0 + 4 * q;
-                    if (q < a.NL && rowok && (unsigned)col < (unsigned)a.W)
+                    floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
+                    if (q < XI::F4 && rowok && (unsigned)col < (unsigned)a.W)
                         x4 = *reinterpret_cast<const floatx4*>(src + col);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) w[4 * q + j] = x4[j];
                 }
-                for (int s = 0; s < a.S; ++s) {
-                    float v[8];
-                    pick8<SW>(w, xc0 - xb + s, v);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (8 * m + j >= valid_cols) v[j] = 0.f;  // columns past the output
-                    *reinterpret_cast<half8*>(xl + (s * 32 + cl) * a.x_plane + row * a.WC8 + 8 * m) =
-                        pack8(v);
+                half_t* const dst = xl + cl * a.x_plane + row * a.WC8;
+                const int plane = 32 * a.x_plane;
+                switch (xc0 - xb) {  // uniform across the block
+                    case 0: write_shifts<0, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
+                    case 1: write_shifts<1, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
+                    case 2: write_shifts<2, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
+                    default: write_shifts<3, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
                 }
             }
             __syncthreads();
@@ -430,6 +503,7 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
             for (int ks = 0; ks < a.KS; ++ks) {
                 const int px0 = ks * 32 + 8 * (lane >> 4);
                 const int ohl = px0 / a.WC8, owl = px0 - ohl * a.WC8;
+                const int pix = ohl * a.sh * a.WC8 + owl;   // X-plane offset of this pixel chunk
                 half8 fa[4];
 #pragma unroll
                 for (int fg = 0; fg < 4; ++fg)
@@ -437,14 +511,8 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
                                                              px0);
 #pragma unroll
                 for (int i = 0; i < NGW; ++i) {
-                    const int g = wave * NGW + i;
-                    if (g >= NG) continue;
-                    const int tap = g / cgroups, cq = g - tap * cgroups;
-                    if ((cq >> 1) != ch) continue;
-                    const int cl = (cq & 1) * 16 + (lane & 15);
-                    const int r = tap / a.S, s = tap - r * a.S;
-                    const half8 fb = *reinterpret_cast<const half8*>(
-                        xl + (s * 32 + cl) * a.x_plane + (ohl * a.sh + r) * a.WC8 + owl);
+                    if (bchunk[i] != ch) continue;  // uniform across the wave
+                    const half8 fb = *reinterpret_cast<const half8*>(xl + boff[i] + pix);
 #pragma unroll
                     for (int fg = 0; fg < 4; ++fg) acc[fg][i] = mfma16x16x32(fa[fg], fb, acc[fg][i]);
                 }
@@ -467,21 +535,47 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
     }
 }
 
-// dW[f, c, r, s] = sum over splits (in order) of the partials.
-__global__ void wgrad_reduce(const float* __restrict__ part, float* __restrict__ dW, int F, int C,
-                             int R, int S, int CT, int nctile, int nsplit) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t total = (int64_t)F * C * R * S;
-    if (i >= total) return;
-    const int s = (int)(i % S), r = (int)((i / S) % R);
-    const int c = (int)((i / ((int64_t)R * S)) % C), f = (int)(i / ((int64_t)C * R * S));
-    const int ty = (f / 64) * nctile + c / CT;
+// dW[f, c, r, s] = sum over splits of the partials, in a fixed order. A block
+// covers 64 consecutive partial columns (contiguous reads across the wave)
+// and four groups of splits; each thread sums its group with several loads in
+// flight, then the four group sums are added in LDS in group order.
+constexpr int kRedCols = 64, kRedGroups = 4;
+__global__ __launch_bounds__(kRedCols * kRedGroups) void wgrad_reduce(
+    const float* __restrict__ part, float* __restrict__ dW, int F, int C, int R, int S, int CT,
+    int nctile, int ntiles, int nsplit) {
+    __shared__ float red[kRedGroups][kRedCols];
     const int ntot = CT * R * S;
-    const int n = (r * S + s) * CT + c % CT;
-    const float* p = part + ((int64_t)ty * nsplit * 64 + (f % 64)) * ntot + n;
+    const int col = threadIdx.x % kRedCols, grp = threadIdx.x / kRedCols;
+    const int64_t i = (int64_t)blockIdx.x * kRedCols + col;
+    const bool live = i < (int64_t)ntiles * 64 * ntot;
+    const int n = live ? (int)(i % ntot) : 0;
+    const int f64 = live ? (int)((i / ntot) % 64) : 0;
+    const int ty = live ? (int)(i / ((int64_t)64 * ntot)) : 0;
+    const float* p = part + ((int64_t)ty * nsplit * 64 + f64) * ntot + n;
+    const int64_t zstride = (int64_t)64 * ntot;
+    const int per = (nsplit + kRedGroups - 1) / kRedGroups;
+    const int z0 = grp * per, z1 = min(nsplit, z0 + per);
     float acc = 0.f;
-    for (int z = 0; z < nsplit; ++z) acc += p[(int64_t)z * 64 * ntot];
-    dW[i] = acc;
+    if (live) {
+        int z = z0;
+        for (; z + 8 <= z1; z += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p[(z + u) * zstride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; z < z1; ++z) acc += p[z * zstride];
+    }
+    red[grp][col] = acc;
+    __syncthreads();
+    if (grp != 0 || !live) return;
+    float sum = red[0][col];
+#pragma unroll
+    for (int g = 1; g < kRedGroups; ++g) sum += red[g][col];
+    const int f = (ty / nctile) * 64 + f64;
+    const int c = (ty % nctile) * CT + n % CT;
+    if (f < F && c < C) dW[((int64_t)f * C + c) * R * S + n / CT] = sum;
 }
 
 template <int SW>
@@ -619,7 +713,6 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.CT = (R * S <= 9 && C > 32) ? 64 : 32;
     a.nftile = ceil_div(F, 64);
     a.nctile = ceil_div(C, a.CT);
-    a.NL = (3 + S - 1 + 7 * sw + 1 + 3) / 4;
     a.WC8 = (std::min(Wo, 224) + 7) & ~7;
     a.ncb = ceil_div(Wo, a.WC8);
     // Rows per tile: about 224 pixels, TH * WC8 a multiple of 32.
@@ -649,9 +742,10 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.part = static_cast<float*>(ws);
     hipError_t e = sw == 1 ? launch_wgrad_sw<1>(a, ngw, st) : launch_wgrad_sw<2>(a, ngw, st);
     if (e != hipSuccess) return fail_hip(e, "band wgrad launch");
-    const int64_t total = (int64_t)F * C * R * S;
-    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                       a.part, dW, F, C, R, S, a.CT, a.nctile, a.nsplit);
+    const int64_t total = (int64_t)tiles * 64 * ntot;
+    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
+                       dim3(kRedCols * kRedGroups), 0, st, a.part, dW, F, C, R, S, a.CT, a.nctile,
+                       tiles, a.nsplit);
     SEERA_HIP_TRY(hipGetLastError());
     *used = true;
     return SEERA_OK;
