@@ -70,6 +70,7 @@ struct WgradArgs {
     int nrb, ncb, items, ips, nsplit;
     int nftile, nctile, CT;
     int dy_stride;      // halves per filter row of the dY tile
+    int xrow;           // halves per row of a shifted X copy (WC8 rounded to whole items)
     int x_plane;        // halves per (s, channel) plane of the shifted X copies
     int64_t lds_bytes;
 };

@@ -335,33 +335,27 @@ __device__ __forceinline__ void pick_at(const floatx44& w, float (&v)[8]) {
 }
 
 // Writes octets OC.. of one X item into shifted copy O - (band alignment):
-// octet m = grp*OCT + OC holds w[O + 8*OC*SW + j*SW], zeroed past the output.
+// octet m = grp*OCT + OC holds w[O + 8*OC*SW + j*SW]. Copy rows are padded to
+// a whole number of items (xrow), so every octet of an item has a slot.
 template <int O, int OC, int SW, int OCT>
-__device__ __forceinline__ void write_octets(const floatx44& w, int grp, int noct,
-                                             int valid_cols, half_t* dst) {
+__device__ __forceinline__ void write_octets(const floatx44& w, int grp, half_t* dst) {
     if constexpr (OC < OCT) {
-        const int m = grp * OCT + OC;
         float v[8];
         pick_at<O + 8 * OC * SW, SW>(w, v);
-        if (8 * m + 8 > valid_cols) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (8 * m + j >= valid_cols) v[j] = 0.f;
-        }
-        if (m < noct) *reinterpret_cast<half8*>(dst + 8 * m) = pack8(v);
-        write_octets<O, OC + 1, SW, OCT>(w, grp, noct, valid_cols, dst);
+        *reinterpret_cast<half8*>(dst + 8 * (grp * OCT + OC)) = pack8(v);
+        write_octets<O, OC + 1, SW, OCT>(w, grp, dst);
     }
 }
 
 // Writes the S (<= 7) tap-shifted copies of one X item; OFF is the band's
 // column alignment (0..3), so every register index is a compile-time constant.
 template <int OFF, int SI, int SW, int OCT>
-__device__ __forceinline__ void write_shifts(const floatx44& w, int S, int grp, int noct,
-                                             int valid_cols, half_t* dst, int plane) {
+__device__ __forceinline__ void write_shifts(const floatx44& w, int S, int grp, half_t* dst,
+                                             int plane) {
     if constexpr (SI < 7) {
         if (SI < S) {
-            write_octets<OFF + SI, 0, SW, OCT>(w, grp, noct, valid_cols, dst + SI * plane);
-            write_shifts<OFF, SI + 1, SW, OCT>(w, S, grp, noct, valid_cols, dst, plane);
+            write_octets<OFF + SI, 0, SW, OCT>(w, grp, dst + SI * plane);
+            write_shifts<OFF, SI + 1, SW, OCT>(w, S, grp, dst, plane);
         }
     }
 }
@@ -404,7 +398,7 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
         const int tap = g / cgroups, cq = g - tap * cgroups;
         const int r = tap / a.S, sh_ = tap - r * a.S;
         bchunk[i] = g < NG ? (cq >> 1) : -1;
-        boff[i] = (sh_ * 32 + (cq & 1) * 16 + (lane & 15)) * a.x_plane + r * a.WC8;
+        boff[i] = (sh_ * 32 + (cq & 1) * 16 + (lane & 15)) * a.x_plane + r * a.xrow;
     }
 
     const int it0 = split * a.ips, it1 = min(a.items, it0 + a.ips);
@@ -489,13 +483,25 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) w[4 * q + j] = x4[j];
                 }
-                half_t* const dst = xl + cl * a.x_plane + row * a.WC8;
+                half_t* const dst = xl + cl * a.x_plane + row * a.xrow;
                 const int plane = 32 * a.x_plane;
                 switch (xc0 - xb) {  // uniform across the block
-                    case 0: write_shifts<0, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
-                    case 1: write_shifts<1, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
-                    case 2: write_shifts<2, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
-                    default: write_shifts<3, 0, SW, XI::OCT>(w, a.S, grp, noct, valid_cols, dst, plane); break;
+                    case 0: write_shifts<0, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
+                    case 1: write_shifts<1, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
+                    case 2: write_shifts<2, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
+                    default: write_shifts<3, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
+                }
+            }
+            if (valid_cols < a.WC8) {
+                // Edge tile: zero the copy columns past the output width (their
+                // dY is zero; keep 0 * inf from turning into NaN).
+                __syncthreads();
+                const int nz = a.WC8 - valid_cols;
+                const int zitems = a.S * 32 * a.BR * nz;
+                for (int z = tid; z < zitems; z += kNT) {
+                    const int col = valid_cols + z % nz;
+                    const int rest = z / nz;
+                    xl[(rest / a.BR) * a.x_plane + (rest % a.BR) * a.xrow + col] = (half_t)0.f;
                 }
             }
             __syncthreads();
@@ -503,7 +509,7 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
             for (int ks = 0; ks < a.KS; ++ks) {
                 const int px0 = ks * 32 + 8 * (lane >> 4);
                 const int ohl = px0 / a.WC8, owl = px0 - ohl * a.WC8;
-                const int pix = ohl * a.sh * a.WC8 + owl;   // X-plane offset of this pixel chunk
+                const int pix = ohl * a.sh * a.xrow + owl;  // X-plane offset of this pixel chunk
                 half8 fa[4];
 #pragma unroll
                 for (int fg = 0; fg < 4; ++fg)
@@ -716,6 +722,7 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.WC8 = (std::min(Wo, 224) + 7) & ~7;
     a.ncb = ceil_div(Wo, a.WC8);
     // Rows per tile: about 224 pixels, TH * WC8 a multiple of 32.
+    const int oct = sw == 1 ? 4 : 2;  // octets per X item (XItem<sw>::OCT)
     const int th_mult = a.WC8 % 32 == 0 ? 1 : a.WC8 % 16 == 0 ? 2 : 4;
     int th = std::max(1, std::min(Ho, 224 / a.WC8));
     th = (th + th_mult - 1) / th_mult * th_mult;
@@ -724,7 +731,8 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
         a.TH = th;
         a.BR = (th - 1) * sh + R;
         a.dy_stride = stride16(th * a.WC8);
-        a.x_plane = stride16(a.BR * a.WC8);
+        a.xrow = (a.WC8 + 8 * oct - 1) / (8 * oct) * (8 * oct);
+        a.x_plane = stride16(a.BR * a.xrow);
         a.lds_bytes = 2 * ((int64_t)64 * a.dy_stride + (int64_t)S * 32 * a.x_plane);
         if (a.lds_bytes <= kBandMaxLds) break;
     }
