@@ -360,9 +360,7 @@ __device__ __forceinline__ void write_shifts(const floatx44& w, int S, int grp, 
     }
 }
 
-constexpr int kDyBatch = 4;  // dY items (2 float4 each) in flight per thread
-
-// X item = kXOct 8-column octets of one channel row; the float4 loads cover
+// X item = OCT 8-column octets of one channel row; its F4 float4 loads cover
 // the octets' columns for every tap shift (offset <= 3 + S - 1 <= 9, S <= 7).
 template <int SW>
 struct XItem {
@@ -370,110 +368,240 @@ struct XItem {
     static constexpr int F4 = (9 + (8 * OCT - 1) * SW + 1 + 3) / 4;
 };
 
-template <int NGW, int SW>
-__global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
+// As write_octets, zeroing the columns >= valid_cols (edge tiles only).
+template <int O, int OC, int SW, int OCT>
+__device__ __forceinline__ void write_octets_edge(const floatx44& w, int grp, int valid_cols,
+                                                  half_t* dst) {
+    if constexpr (OC < OCT) {
+        const int m = grp * OCT + OC;
+        float v[8];
+        pick_at<O + 8 * OC * SW, SW>(w, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (8 * m + j >= valid_cols) v[j] = 0.f;
+        *reinterpret_cast<half8*>(dst + 8 * m) = pack8(v);
+        write_octets_edge<O, OC + 1, SW, OCT>(w, grp, valid_cols, dst);
+    }
+}
+
+template <int OFF, int SI, int SW, int OCT>
+__device__ __forceinline__ void write_shifts_edge(const floatx44& w, int S, int grp,
+                                                  int valid_cols, half_t* dst, int plane) {
+    if constexpr (SI < 7) {
+        if (SI < S) {
+            write_octets_edge<OFF + SI, 0, SW, OCT>(w, grp, valid_cols, dst + SI * plane);
+            write_shifts_edge<OFF, SI + 1, SW, OCT>(w, S, grp, valid_cols, dst, plane);
+        }
+    }
+}
+
+constexpr int kWgNT = 512;    // 4 consumer waves (MFMA) + 4 producer waves (loads, fp16 copies)
+constexpr int kWgProd = 256;  // producer threads
+constexpr int kWgDyMax = 4;   // dY items (8 columns of one filter row) per producer thread
+constexpr int kWgKsMax = 7;   // 32-pixel k-steps per tile
+
+// Warp-specialised pipeline over steps (tile, 32-channel chunk) of this block.
+// At step k the consumer waves run the MFMAs of step k from LDS stage k&1
+// while the producer waves write step k+1 (fp16 dY tile on a tile's first
+// chunk, S shifted fp16 X copies) into stage (k+1)&1 from registers loaded
+// during step k-1, then issue the global loads of step k+2. One barrier per
+// step; a consumer and a producer share each SIMD, so the conversion VALU
+// work and the MFMAs run side by side and HBM loads stay in flight.
+template <int NGW, int SW, int NCH>
+__global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
+    using XI = XItem<SW>;
+    static_assert(XI::F4 <= 11, "window exceeds 44 floats");
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
-    half_t* const dyl = smem;                      // 64 x dy_stride
-    half_t* const xl = smem + 64 * a.dy_stride;    // S x 32 x x_plane
+    const int dy_stage = 64 * a.dy_stride;              // halves per dY buffer
+    const int x_stage = a.S * 32 * a.x_plane;           // halves per X copies buffer
+    half_t* const dyb = smem;                           // [2] dY tile, by tile parity
+    half_t* const xb2 = smem + 2 * dy_stage;            // [2] X copies, by step parity
 
     const int split = blockIdx.x, ty = blockIdx.y;
     const int ftile = ty / a.nctile, ctile = ty - ftile * a.nctile;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int NG = a.CT * a.R * a.S / 16;
-    const int cgroups = a.CT / 16;
-    const int noct = a.WC8 >> 3;
+    const bool consumer = wave < 4;
+    const int it0 = split * a.ips, it1 = min(a.items, it0 + a.ips);
+    const int nsteps = max(0, it1 - it0) * NCH;
 
-    floatx4_t acc[4][NGW];
-#pragma unroll
-    for (int fg = 0; fg < 4; ++fg)
-#pragma unroll
-        for (int i = 0; i < NGW; ++i) acc[fg][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    auto tile_b = [&](int item) { return item / a.ncb / a.nrb; };
+    auto tile_oh0 = [&](int item) { return (item / a.ncb % a.nrb) * a.TH; };
+    auto tile_ow0 = [&](int item) { return item % a.ncb * a.WC8; };
+    auto floor4 = [](int v) { return v >= 0 ? (v & ~3) : -((-v + 3) & ~3); };
 
-    // Per n-group of this wave: LDS offset of this lane's B fragment at pixel
-    // (0, 0) and the 32-channel chunk the group belongs to (-1: no group).
-    int boff[NGW], bchunk[NGW];
+    if (consumer) {
+        // ---------------- consumer: MFMAs ----------------
+        const int ngc = 2 * a.R * a.S;                  // 16-channel groups per chunk
+        int boff[NGW];
+        bool gon[NGW];
 #pragma unroll
-    for (int i = 0; i < NGW; ++i) {
-        const int g = wave * NGW + i;
-        const int tap = g / cgroups, cq = g - tap * cgroups;
-        const int r = tap / a.S, sh_ = tap - r * a.S;
-        bchunk[i] = g < NG ? (cq >> 1) : -1;
-        boff[i] = (sh_ * 32 + (cq & 1) * 16 + (lane & 15)) * a.x_plane + r * a.xrow;
+        for (int i = 0; i < NGW; ++i) {
+            const int g = wave + 4 * i;
+            const int tap = g >> 1, half = g & 1;
+            const int r = tap / a.S, sc = tap - r * a.S;
+            gon[i] = g < ngc;
+            boff[i] = (sc * 32 + half * 16 + (lane & 15)) * a.x_plane + r * a.xrow;
+        }
+        int apx[kWgKsMax], xpix[kWgKsMax];
+#pragma unroll
+        for (int ks = 0; ks < kWgKsMax; ++ks) {
+            const int px0 = ks * 32 + 8 * (lane >> 4);
+            const int ohl = px0 / a.WC8, owl = px0 - ohl * a.WC8;
+            apx[ks] = px0;
+            xpix[ks] = ohl * a.sh * a.xrow + owl;
+        }
+        floatx4_t acc[NCH][NGW][4];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < NGW; ++i)
+#pragma unroll
+                for (int fg = 0; fg < 4; ++fg) acc[c][i][fg] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+        __syncthreads();  // stage 0 written
+        for (int k = 0; k < nsteps; ++k) {
+            const int item = it0 + k / NCH;
+            const half_t* const dyl = dyb + ((item - it0) & 1) * dy_stage;
+            const half_t* const xl = xb2 + (k & 1) * x_stage;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                if (c != k % NCH) continue;
+#pragma unroll
+                for (int ks = 0; ks < kWgKsMax; ++ks) {
+                    if (ks >= a.KS) break;
+                    half8 fa[4], fb[NGW];
+#pragma unroll
+                    for (int fg = 0; fg < 4; ++fg)
+                        fa[fg] = *reinterpret_cast<const half8*>(
+                            dyl + (fg * 16 + (lane & 15)) * a.dy_stride + apx[ks]);
+#pragma unroll
+                    for (int i = 0; i < NGW; ++i)
+                        if (gon[i]) fb[i] = *reinterpret_cast<const half8*>(xl + boff[i] + xpix[ks]);
+#pragma unroll
+                    for (int i = 0; i < NGW; ++i) {
+                        if (!gon[i]) continue;
+#pragma unroll
+                        for (int fg = 0; fg < 4; ++fg)
+                            acc[c][i][fg] = mfma16x16x32(fa[fg], fb[i], acc[c][i][fg]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        // Partial sums: part[ty][split][f64][n], n = tap * CT + channel in the tile.
+        const int ntot = a.CT * a.R * a.S;
+        float* const dst = a.part + ((int64_t)ty * a.nsplit + split) * 64 * ntot;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < NGW; ++i) {
+                if (!gon[i]) continue;
+                const int g = wave + 4 * i;
+                const int n = (g >> 1) * a.CT + c * 32 + (g & 1) * 16 + (lane & 15);
+#pragma unroll
+                for (int fg = 0; fg < 4; ++fg)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        dst[(int64_t)(fg * 16 + 4 * (lane >> 4) + r) * ntot + n] = acc[c][i][fg][r];
+            }
+        return;
     }
 
-    const int it0 = split * a.ips, it1 = min(a.items, it0 + a.ips);
-    for (int item = it0; item < it1; ++item) {
-        int rem = item;
-        const int cb = rem % a.ncb;
-        rem /= a.ncb;
-        const int rb = rem % a.nrb;
-        const int b = rem / a.nrb;
-        const int oh0 = rb * a.TH, ow0 = cb * a.WC8;
-        const int valid_cols = a.Wo - ow0;
+    // ---------------- producer: loads and fp16 copies ----------------
+    const int ptid = tid - 256;
+    const int noct = a.WC8 >> 3;
+    const int ngrp = (noct + XI::OCT - 1) / XI::OCT;
+    const int dy_items = 64 * a.TH * noct;
+    const int x_items = 32 * a.BR * ngrp;
+    const int f_lim = a.F - ftile * 64;
+    int dyit[kWgDyMax];
+#pragma unroll
+    for (int kk = 0; kk < kWgDyMax; ++kk) {
+        const int it = ptid + kk * kWgProd;
+        const int m = it % noct, rest = it / noct;
+        dyit[kk] = it < dy_items ? ((rest / a.TH) | (rest % a.TH) << 8 | m << 16) : -1;
+    }
+    int xit = -1;
+    if (ptid < x_items) {
+        const int grp = ptid % ngrp, rest = ptid / ngrp;
+        xit = (rest / a.BR) | (rest % a.BR) << 8 | grp << 16;
+    }
+    floatx4 dyv[kWgDyMax][2];
+    floatx44 xw;
 
-        __syncthreads();  // previous tile's MFMAs are done with LDS
-        // dY tile: 64 filters x TH rows x WC8 columns, 8 columns per item. Each
-        // thread issues the loads of kDyBatch items before converting any, so
-        // that many loads are in flight.
-        const int dy_items = 64 * a.TH * noct;
-        for (int it0 = tid; it0 < dy_items; it0 += kNT * kDyBatch) {
-            floatx4 v[kDyBatch][2];
+    // Iteration j (-1 .. nsteps-1): write step j (registers -> LDS stage j&1),
+    // then issue the global loads of step j+1 into the registers, then meet
+    // the consumers at the barrier that releases step j to them.
+    for (int j = -1; j < nsteps; ++j) {
+        if (j >= 0) {
+            const int item = it0 + j / NCH, ch = j % NCH;
+            const int ow0 = tile_ow0(item);
+            if (ch == 0) {
+                half_t* const dyl = dyb + ((item - it0) & 1) * dy_stage;
 #pragma unroll
-            for (int k = 0; k < kDyBatch; ++k) {
-                const int it = it0 + k * kNT;
-                const int m = it % noct;
-                const int rest = it / noct;
-                const int ohl = rest % a.TH, fl = rest / a.TH;
-                const int f = ftile * 64 + fl, oh = oh0 + ohl, ow = ow0 + 8 * m;
-                const float* src = a.dy + (((int64_t)b * a.F + f) * a.Ho + oh) * a.Wo + ow;
+                for (int kk = 0; kk < kWgDyMax; ++kk) {
+                    if (dyit[kk] < 0) continue;
+                    const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16;
+                    float f8[8];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    v[k][h] = floatx4{0.f, 0.f, 0.f, 0.f};
-                    if (it < dy_items && f < a.F && oh < a.Ho && ow + 4 * h < a.Wo)
-                        v[k][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kDyBatch; ++k) {
-                const int it = it0 + k * kNT;
-                const int m = it % noct;
-                const int rest = it / noct;
-                const int ohl = rest % a.TH, fl = rest / a.TH;
-                float f8[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f8[j] = v[k][0][j];
-                    f8[4 + j] = v[k][1][j];
-                }
-                if (it < dy_items)
+                    for (int q = 0; q < 4; ++q) {
+                        f8[q] = dyv[kk][0][q];
+                        f8[4 + q] = dyv[kk][1][q];
+                    }
                     *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) =
                         pack8(f8);
+                }
+            }
+            if (xit >= 0) {
+                const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;
+                half_t* const dst = xb2 + (j & 1) * x_stage + cl * a.x_plane + row * a.xrow;
+                const int plane = 32 * a.x_plane;
+                const int xc0 = ow0 * a.sw - a.pw;
+                const int valid_cols = a.Wo - ow0;
+                if (valid_cols >= a.WC8) {
+                    switch (xc0 - floor4(xc0)) {  // uniform across the block
+                        case 0: write_shifts<0, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
+                        case 1: write_shifts<1, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
+                        case 2: write_shifts<2, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
+                        default: write_shifts<3, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
+                    }
+                } else {
+                    // Edge tile: columns past the output width get 0 (their dY
+                    // is zero; this keeps 0 * inf from turning into NaN).
+                    switch (xc0 - floor4(xc0)) {
+                        case 0: write_shifts_edge<0, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
+                        case 1: write_shifts_edge<1, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
+                        case 2: write_shifts_edge<2, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
+                        default: write_shifts_edge<3, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
+                    }
+                }
             }
         }
-
-        const int ir0 = oh0 * a.sh - a.ph;
-        const int xc0 = ow0 * a.sw - a.pw;                     // X column of (ow0, s = 0)
-        const int xb = xc0 >= 0 ? (xc0 & ~3) : -((-xc0 + 3) & ~3);
-        const int nchunk = a.CT / 32;
-        for (int ch = 0; ch < nchunk; ++ch) {
-            if (ch > 0) __syncthreads();
-            // Shifted X copies for channels [cbase, cbase + 32). An item is
-            // XItem::OCT octets of one channel row: its XItem::F4 float4 loads
-            // are all issued before any copy is written.
-            using XI = XItem<SW>;
-            const int cbase = ctile * a.CT + ch * 32;
-            const int ngrp = (noct + XI::OCT - 1) / XI::OCT;
-            const int x_items = 32 * a.BR * ngrp;
-            for (int it = tid; it < x_items; it += kNT) {
-                const int grp = it % ngrp;
-                const int rest = it / ngrp;
-                const int row = rest % a.BR, cl = rest / a.BR;
-                const int c = cbase + cl, hin = ir0 + row;
-                const int a0 = xb + 8 * XI::OCT * grp * SW;
+        if (j + 1 < nsteps) {
+            const int item = it0 + (j + 1) / NCH, ch = (j + 1) % NCH;
+            const int b = tile_b(item), oh0 = tile_oh0(item), ow0 = tile_ow0(item);
+            if (ch == 0) {
+#pragma unroll
+                for (int kk = 0; kk < kWgDyMax; ++kk) {
+                    const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16;
+                    const int oh = oh0 + ohl, ow = ow0 + 8 * m;
+                    const bool ok = dyit[kk] >= 0 && fl < f_lim && oh < a.Ho;
+                    const float* src =
+                        a.dy + (((int64_t)b * a.F + ftile * 64 + fl) * a.Ho + oh) * a.Wo + ow;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        dyv[kk][h] = floatx4{0.f, 0.f, 0.f, 0.f};
+                        if (ok && ow + 4 * h < a.Wo)
+                            dyv[kk][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
+                    }
+                }
+            }
+            if (xit >= 0) {
+                const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;
+                const int c = ctile * a.CT + ch * 32 + cl, hin = oh0 * a.sh - a.ph + row;
+                const int a0 = floor4(ow0 * a.sw - a.pw) + 8 * XI::OCT * grp * SW;
                 const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;
                 const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;
-                static_assert(XI::F4 <= 11, "window exceeds 44 floats");
-                floatx44 w;
 #pragma unroll
                 for (int q = 0; q < 11; ++q) {
                     const int col = a0 + 4 * q;
@@ -481,64 +609,14 @@ __global__ __launch_bounds__(kNT) void band_wgrad_kernel(const WgradArgs a) {
                     if (q < XI::F4 && rowok && (unsigned)col < (unsigned)a.W)
                         x4 = *reinterpret_cast<const floatx4*>(src + col);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) w[4 * q + j] = x4[j];
-                }
-                half_t* const dst = xl + cl * a.x_plane + row * a.xrow;
-                const int plane = 32 * a.x_plane;
-                switch (xc0 - xb) {  // uniform across the block
-                    case 0: write_shifts<0, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
-                    case 1: write_shifts<1, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
-                    case 2: write_shifts<2, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
-                    default: write_shifts<3, 0, SW, XI::OCT>(w, a.S, grp, dst, plane); break;
-                }
-            }
-            if (valid_cols < a.WC8) {
-                // Edge tile: zero the copy columns past the output width (their
-                // dY is zero; keep 0 * inf from turning into NaN).
-                __syncthreads();
-                const int nz = a.WC8 - valid_cols;
-                const int zitems = a.S * 32 * a.BR * nz;
-                for (int z = tid; z < zitems; z += kNT) {
-                    const int col = valid_cols + z % nz;
-                    const int rest = z / nz;
-                    xl[(rest / a.BR) * a.x_plane + (rest % a.BR) * a.xrow + col] = (half_t)0.f;
-                }
-            }
-            __syncthreads();
-
-            for (int ks = 0; ks < a.KS; ++ks) {
-                const int px0 = ks * 32 + 8 * (lane >> 4);
-                const int ohl = px0 / a.WC8, owl = px0 - ohl * a.WC8;
-                const int pix = ohl * a.sh * a.xrow + owl;  // X-plane offset of this pixel chunk
-                half8 fa[4];
-#pragma unroll
-                for (int fg = 0; fg < 4; ++fg)
-                    fa[fg] = *reinterpret_cast<const half8*>(dyl + (fg * 16 + (lane & 15)) * a.dy_stride +
-                                                             px0);
-#pragma unroll
-                for (int i = 0; i < NGW; ++i) {
-                    if (bchunk[i] != ch) continue;  // uniform across the wave
-                    const half8 fb = *reinterpret_cast<const half8*>(xl + boff[i] + pix);
-#pragma unroll
-                    for (int fg = 0; fg < 4; ++fg) acc[fg][i] = mfma16x16x32(fa[fg], fb, acc[fg][i]);
+                    for (int e = 0; e < 4; ++e) xw[4 * q + e] = x4[e];
                 }
             }
         }
+        if (j >= 0 || nsteps == 0) __syncthreads();
     }
-
-    // Partial sums: part[ty][split][f64][n], n = tap * CT + channel within the tile.
-    const int ntot = a.CT * a.R * a.S;
-    float* const dst = a.part + ((int64_t)ty * a.nsplit + split) * 64 * ntot;
-#pragma unroll
-    for (int i = 0; i < NGW; ++i) {
-        const int g = wave * NGW + i;
-        if (g >= NG) continue;
-        const int n = g * 16 + (lane & 15);
-#pragma unroll
-        for (int fg = 0; fg < 4; ++fg)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) dst[(int64_t)(fg * 16 + 4 * (lane >> 4) + r) * ntot + n] = acc[fg][i][r];
-    }
+    if (nsteps == 0) return;
+    __syncthreads();  // matches the consumers' final barrier
 }
 
 // dW[f, c, r, s] = sum over splits of the partials, in a fixed order. A block
@@ -584,19 +662,18 @@ __global__ __launch_bounds__(kRedCols * kRedGroups) void wgrad_reduce(
     if (f < F && c < C) dW[((int64_t)f * C + c) * R * S + n / CT] = sum;
 }
 
-template <int SW>
+template <int SW, int NCH>
 hipError_t launch_wgrad_sw(const WgradArgs& a, int ngw, hipStream_t st) {
     const void* k = nullptr;
     switch (ngw) {
-        case 1: k = reinterpret_cast<const void*>(band_wgrad_kernel<1, SW>); break;
-        case 2: k = reinterpret_cast<const void*>(band_wgrad_kernel<2, SW>); break;
-        case 3: k = reinterpret_cast<const void*>(band_wgrad_kernel<3, SW>); break;
-        case 4: k = reinterpret_cast<const void*>(band_wgrad_kernel<4, SW>); break;
-        case 5: k = reinterpret_cast<const void*>(band_wgrad_kernel<5, SW>); break;
-        case 6: k = reinterpret_cast<const void*>(band_wgrad_kernel<6, SW>); break;
-        case 7: k = reinterpret_cast<const void*>(band_wgrad_kernel<7, SW>); break;
-        case 8: k = reinterpret_cast<const void*>(band_wgrad_kernel<8, SW>); break;
-        default: k = reinterpret_cast<const void*>(band_wgrad_kernel<9, SW>); break;
+        case 1: k = reinterpret_cast<const void*>(band_wgrad_kernel<1, SW, NCH>); break;
+        case 2: k = reinterpret_cast<const void*>(band_wgrad_kernel<2, SW, NCH>); break;
+        case 3: k = reinterpret_cast<const void*>(band_wgrad_kernel<3, SW, NCH>); break;
+        case 4: k = reinterpret_cast<const void*>(band_wgrad_kernel<4, SW, NCH>); break;
+        case 5: k = reinterpret_cast<const void*>(band_wgrad_kernel<5, SW, NCH>); break;
+        case 6: k = reinterpret_cast<const void*>(band_wgrad_kernel<6, SW, NCH>); break;
+        case 7: k = reinterpret_cast<const void*>(band_wgrad_kernel<7, SW, NCH>); break;
+        default: k = reinterpret_cast<const void*>(band_wgrad_kernel<8, SW, NCH>); break;
     }
     if (a.lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -604,7 +681,7 @@ hipError_t launch_wgrad_sw(const WgradArgs& a, int ngw, hipStream_t st) {
         if (e != hipSuccess) return e;
     }
     void* args[] = {const_cast<WgradArgs*>(&a)};
-    return hipLaunchKernel(k, dim3(a.nsplit, a.nftile * a.nctile), dim3(kNT), args,
+    return hipLaunchKernel(k, dim3(a.nsplit, a.nftile * a.nctile), dim3(kWgNT), args,
                            (size_t)a.lds_bytes, st);
 }
 
@@ -716,27 +793,48 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.dy = Y; a.x = X;
     a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Ho = Ho; a.Wo = Wo;
     a.R = R; a.S = S; a.sh = sh; a.sw = sw; a.ph = ph; a.pw = pw;
+    // Channels per block tile: two 32-channel chunks when the consumer
+    // accumulators (2 chunks x ceil(2*R*S/4) groups x 16 floats) fit.
     a.CT = (R * S <= 9 && C > 32) ? 64 : 32;
+    const int nch = a.CT / 32;
+    const int ngw = ceil_div(2 * R * S, 4);
+    if (ngw > 8) return SEERA_OK;
     a.nftile = ceil_div(F, 64);
     a.nctile = ceil_div(C, a.CT);
-    a.WC8 = (std::min(Wo, 224) + 7) & ~7;
-    a.ncb = ceil_div(Wo, a.WC8);
-    // Rows per tile: about 224 pixels, TH * WC8 a multiple of 32.
+    // Output tile TH x WC8 (TH * WC8 a multiple of 32): the largest one whose
+    // producer loads fit the per-thread budgets and whose two LDS stages fit.
     const int oct = sw == 1 ? 4 : 2;  // octets per X item (XItem<sw>::OCT)
-    const int th_mult = a.WC8 % 32 == 0 ? 1 : a.WC8 % 16 == 0 ? 2 : 4;
-    int th = std::max(1, std::min(Ho, 224 / a.WC8));
-    th = (th + th_mult - 1) / th_mult * th_mult;
-    for (;; th -= th_mult) {
-        if (th < th_mult) return SEERA_OK;
-        a.TH = th;
-        a.BR = (th - 1) * sh + R;
-        a.dy_stride = stride16(th * a.WC8);
-        a.xrow = (a.WC8 + 8 * oct - 1) / (8 * oct) * (8 * oct);
-        a.x_plane = stride16(a.BR * a.xrow);
-        a.lds_bytes = 2 * ((int64_t)64 * a.dy_stride + (int64_t)S * 32 * a.x_plane);
-        if (a.lds_bytes <= kBandMaxLds) break;
+    const int wo_cap = std::min(Wo, 224);
+    const int wc_opts[2] = {(wo_cap + 7) & ~7, (wo_cap + 31) & ~31};
+    int best_px = 0;
+    WgradArgs best = a;
+    for (int wc : wc_opts) {
+        const int noct = wc / 8, ngrp = ceil_div(noct, oct);
+        const int th_mult = wc % 32 == 0 ? 1 : wc % 16 == 0 ? 2 : 4;
+        for (int th = th_mult; th * wc <= kWgKsMax * 32; th += th_mult) {
+            WgradArgs t = a;
+            t.WC8 = wc;
+            t.TH = th;
+            t.BR = (th - 1) * sh + R;
+            t.dy_stride = stride16(th * wc);
+            t.xrow = ceil_div(wc, 8 * oct) * 8 * oct;
+            t.x_plane = stride16(t.BR * t.xrow);
+            t.lds_bytes = 2 * 2 * ((int64_t)64 * t.dy_stride + (int64_t)S * 32 * t.x_plane);
+            const bool fits = t.lds_bytes <= kBandMaxLds && 64 * th * noct <= kWgDyMax * kWgProd &&
+                              32 * t.BR * ngrp <= kWgProd;
+            if (!fits) break;
+            const int px = std::min(th, Ho) * std::min(wc, Wo);  // useful pixels
+            if (px > best_px) {
+                best_px = px;
+                best = t;
+            }
+            if (th >= Ho) break;
+        }
     }
+    if (best_px == 0) return SEERA_OK;
+    a = best;
     a.KS = a.TH * a.WC8 / 32;
+    a.ncb = ceil_div(Wo, a.WC8);
     a.nrb = ceil_div(Ho, a.TH);
     a.items = B * a.nrb * a.ncb;
     const int tiles = a.nftile * a.nctile;
@@ -744,11 +842,12 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.ips = ceil_div(a.items, nsplit);
     a.nsplit = ceil_div(a.items, a.ips);
     const int ntot = a.CT * R * S;
-    const int ngw = ceil_div(ntot / 16, 4);
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(float) * (size_t)tiles * a.nsplit * 64 * ntot, &ws));
     a.part = static_cast<float*>(ws);
-    hipError_t e = sw == 1 ? launch_wgrad_sw<1>(a, ngw, st) : launch_wgrad_sw<2>(a, ngw, st);
+    hipError_t e;
+    if (sw == 1) e = nch == 2 ? launch_wgrad_sw<1, 2>(a, ngw, st) : launch_wgrad_sw<1, 1>(a, ngw, st);
+    else e = nch == 2 ? launch_wgrad_sw<2, 2>(a, ngw, st) : launch_wgrad_sw<2, 1>(a, ngw, st);
     if (e != hipSuccess) return fail_hip(e, "band wgrad launch");
     const int64_t total = (int64_t)tiles * 64 * ntot;
     hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
