@@ -521,10 +521,13 @@ __global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
         const int m = it % noct, rest = it / noct;
         dyit[kk] = it < dy_items ? ((rest / a.TH) | (rest % a.TH) << 8 | m << 16) : -1;
     }
+    // Channel fastest across lanes: the copy planes of consecutive channels are
+    // 16 bytes apart modulo 128, so a wave's 16-byte copy writes spread over
+    // all banks.
     int xit = -1;
     if (ptid < x_items) {
-        const int grp = ptid % ngrp, rest = ptid / ngrp;
-        xit = (rest / a.BR) | (rest % a.BR) << 8 | grp << 16;
+        const int cl = ptid % 32, rest = ptid / 32;
+        xit = cl | (rest % a.BR) << 8 | (rest / a.BR) << 16;
     }
     floatx4 dyv[kWgDyMax][2];
     floatx44 xw;
