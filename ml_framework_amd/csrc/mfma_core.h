@@ -246,22 +246,36 @@ __device__ __forceinline__ void read_frags(const half_t* As, const half_t* Bs, i
     for (int j = 0; j < TN; ++j) b[j] = lds_read8<BK>(Bs, wn0 + j * 32 + (lane & 31), chunk);
 }
 
-template <int BK, int TM, int TN>
+template <int BK, int TM, int TN, bool PREFETCH = true>
 __device__ __forceinline__ void mfma_slice(const half_t* As, const half_t* Bs, int wm0,
                                            int wn0, int lane, floatx16 (&acc)[TM][TN]) {
     constexpr int KK = BK / 16;
-    half8 a[2][TM], b[2][TN];
-    read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, 0, a[0], b[0]);
+    if constexpr (PREFETCH) {
+        half8 a[2][TM], b[2][TN];
+        read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, 0, a[0], b[0]);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-        if (kk + 1 < KK)
-            read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, kk + 1, a[(kk + 1) & 1],
-                                   b[(kk + 1) & 1]);
+        for (int kk = 0; kk < KK; ++kk) {
+            if (kk + 1 < KK)
+                read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, kk + 1, a[(kk + 1) & 1],
+                                       b[(kk + 1) & 1]);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = mfma32x32x16(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = mfma32x32x16(a[kk & 1][i], b[kk & 1][j], acc[i][j]);
+        }
+    } else {
+        // One fragment set: for waves whose register budget is tight; another
+        // wave on the SIMD covers the LDS latency.
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            half8 a[TM], b[TN];
+            read_frags<BK, TM, TN>(As, Bs, wm0, wn0, lane, kk, a, b);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16(a[i], b[j], acc[i][j]);
+        }
     }
 }
 

@@ -9,8 +9,8 @@
 namespace seera {
 
 // Block-tile shapes (BM x BN x BK, wave grid):
-//   L   256x256x64, 2x4 waves of 128x64  large GEMMs (two waves per SIMD hide
-//                                         each other's LDS and load stalls)
+//   L   256x256x32, warp-specialised: 4x2 consumer waves of 64x128 run the
+//       MFMAs while 4 producer waves load and round the next K slice
 //   W   64x256x32,  1x4 waves of 64x64  few rows (conv output channels)
 //   M   128x128x32, 2x2 waves of 64x64
 //   S   64x64x32,   2x2 waves of 32x32  small / odd shapes, scalar loads
@@ -25,7 +25,7 @@ struct Plan {
 constexpr int kNumCUs = 256;
 constexpr int kBK = 32;      // split-K slice granularity (slice ends are predicated, so it need
                              // not be a multiple of the tile BK; it is a multiple of 4 floats)
-constexpr int kMaxBK = 64;   // deepest K slice of any tile (tile span checks)
+constexpr int kMaxBK = 32;   // deepest K slice of any tile (tile span checks)
 
 inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
 inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
@@ -78,7 +78,7 @@ template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
     if constexpr (BIG) {
         switch (t) {
-            case Tile::L: return launch_igemm<256, 256, 64, 2, 4>(p, splits, st);
+            case Tile::L: return launch_igemm_ws<256, 256, 32, 4, 2, 4>(p, splits, st);
             case Tile::W: return launch_igemm<64, 256, 32, 1, 4>(p, splits, st);
             case Tile::M: return launch_igemm<128, 128, 32, 2, 2>(p, splits, st);
             default: break;
