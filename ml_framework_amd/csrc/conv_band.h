@@ -55,6 +55,12 @@ int band_conv_dgrad(const float* Y, const float* W, float* out, int B, int Fc, i
                     int Cc, int H, int W_out, int R, int S, int sh, int sw, int ph, int pw,
                     hipStream_t st, bool* used);
 
+// Row-streaming variant (conv_stream.hip) of the launch `band` describes
+// (weights already prepared in band.wk): runs when every phase reads its input
+// with stride 1 and the weights plus an input-row ring fit in LDS; *used
+// reports whether it ran.
+int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used);
+
 }  // namespace seera
 
 namespace seera {

@@ -722,7 +722,9 @@ int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H
     hipLaunchKernelGGL(prep_fwd_weights, dim3((unsigned)((wsz + 255) / 256)), dim3(256), 0, st, Wt,
                        static_cast<half_t*>(ws), F, C, R, S, a.nchunks, wsz);
     SEERA_HIP_TRY(hipGetLastError());
-    SEERA_TRY(launch_band(a, st));
+    bool streamed = false;
+    SEERA_TRY(stream_conv(a, st, &streamed));
+    if (!streamed) SEERA_TRY(launch_band(a, st));
     *used = true;
     return SEERA_OK;
 }
@@ -779,7 +781,9 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
                            ax[z][0].r0, ax[z][1].r0, a.ph[z].T, a.ph[z].U, a.nchunks, n);
         SEERA_HIP_TRY(hipGetLastError());
     }
-    SEERA_TRY(launch_band(a, st));
+    bool streamed = false;
+    SEERA_TRY(stream_conv(a, st, &streamed));
+    if (!streamed) SEERA_TRY(launch_band(a, st));
     *used = true;
     return SEERA_OK;
 }

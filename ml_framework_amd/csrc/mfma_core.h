@@ -62,6 +62,12 @@ __device__ __forceinline__ floatx4 buf_load4(rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
 
+// Per-lane offset plus a wave-uniform one (held in an SGPR). Callers keep
+// voff + soff below 2^32; a lane with voff >= kBufOOB reads 0.
+__device__ __forceinline__ floatx4 buf_load4s(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 __device__ __forceinline__ float buf_load1(rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
