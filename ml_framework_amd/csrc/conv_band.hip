@@ -529,95 +529,107 @@ __global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
         const int cl = ptid % 32, rest = ptid / 32;
         xit = cl | (rest % a.BR) << 8 | (rest / a.BR) << 16;
     }
-    floatx4 dyv[kWgDyMax][2];
-    floatx44 xw;
+    // Two register sets: the loads of step j+2 are issued right after step j
+    // is written, so each load has two consumer steps to arrive.
+    floatx4 dyv0[kWgDyMax][2], dyv1[kWgDyMax][2];
+    floatx44 xw0, xw1;
 
-    // Iteration j (-1 .. nsteps-1): write step j (registers -> LDS stage j&1),
-    // then issue the global loads of step j+1 into the registers, then meet
-    // the consumers at the barrier that releases step j to them.
-    for (int j = -1; j < nsteps; ++j) {
-        if (j >= 0) {
-            const int item = it0 + j / NCH, ch = j % NCH;
-            const int ow0 = tile_ow0(item);
-            if (ch == 0) {
-                half_t* const dyl = dyb + ((item - it0) & 1) * dy_stage;
-#pragma unroll
-                for (int kk = 0; kk < kWgDyMax; ++kk) {
-                    if (dyit[kk] < 0) continue;
-                    const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16;
-                    float f8[8];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        f8[q] = dyv[kk][0][q];
-                        f8[4 + q] = dyv[kk][1][q];
-                    }
-                    *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) =
-                        pack8(f8);
-                }
-            }
-            if (xit >= 0) {
-                const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;
-                half_t* const dst = xb2 + (j & 1) * x_stage + cl * a.x_plane + row * a.xrow;
-                const int plane = 32 * a.x_plane;
-                const int xc0 = ow0 * a.sw - a.pw;
-                const int valid_cols = a.Wo - ow0;
-                if (valid_cols >= a.WC8) {
-                    switch (xc0 - floor4(xc0)) {  // uniform across the block
-                        case 0: write_shifts<0, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
-                        case 1: write_shifts<1, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
-                        case 2: write_shifts<2, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
-                        default: write_shifts<3, 0, SW, XI::OCT>(xw, a.S, grp, dst, plane); break;
-                    }
-                } else {
-                    // Edge tile: columns past the output width get 0 (their dY
-                    // is zero; this keeps 0 * inf from turning into NaN).
-                    switch (xc0 - floor4(xc0)) {
-                        case 0: write_shifts_edge<0, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
-                        case 1: write_shifts_edge<1, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
-                        case 2: write_shifts_edge<2, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
-                        default: write_shifts_edge<3, 0, SW, XI::OCT>(xw, a.S, grp, valid_cols, dst, plane); break;
-                    }
-                }
-            }
-        }
-        if (j + 1 < nsteps) {
-            const int item = it0 + (j + 1) / NCH, ch = (j + 1) % NCH;
-            const int b = tile_b(item), oh0 = tile_oh0(item), ow0 = tile_ow0(item);
-            if (ch == 0) {
-#pragma unroll
-                for (int kk = 0; kk < kWgDyMax; ++kk) {
-                    const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16;
-                    const int oh = oh0 + ohl, ow = ow0 + 8 * m;
-                    const bool ok = dyit[kk] >= 0 && fl < f_lim && oh < a.Ho;
-                    const float* src =
-                        a.dy + (((int64_t)b * a.F + ftile * 64 + fl) * a.Ho + oh) * a.Wo + ow;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        dyv[kk][h] = floatx4{0.f, 0.f, 0.f, 0.f};
-                        if (ok && ow + 4 * h < a.Wo)
-                            dyv[kk][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);
-                    }
-                }
-            }
-            if (xit >= 0) {
-                const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;
-                const int c = ctile * a.CT + ch * 32 + cl, hin = oh0 * a.sh - a.ph + row;
-                const int a0 = floor4(ow0 * a.sw - a.pw) + 8 * XI::OCT * grp * SW;
-                const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;
-                const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;
-#pragma unroll
-                for (int q = 0; q < 11; ++q) {
-                    const int col = a0 + 4 * q;
-                    floatx4 x4 = {0.f, 0.f, 0.f, 0.f};
-                    if (q < XI::F4 && rowok && (unsigned)col < (unsigned)a.W)
-                        x4 = *reinterpret_cast<const floatx4*>(src + col);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) xw[4 * q + e] = x4[e];
-                }
-            }
-        }
-        if (j >= 0 || nsteps == 0) __syncthreads();
+    // Write step J (registers DYV/XW -> LDS stage J&1).
+#define SEERA_WG_WRITE(J, DYV, XW)                                                          \
+    {                                                                                       \
+        const int item = it0 + (J) / NCH, ch = (J) % NCH;                                   \
+        const int ow0 = tile_ow0(item);                                                     \
+        if (ch == 0) {                                                                      \
+            half_t* const dyl = dyb + ((item - it0) & 1) * dy_stage;                        \
+            _Pragma("unroll") for (int kk = 0; kk < kWgDyMax; ++kk) {                       \
+                if (dyit[kk] < 0) continue;                                                 \
+                const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16; \
+                float f8[8];                                                                \
+                _Pragma("unroll") for (int q = 0; q < 4; ++q) {                             \
+                    f8[q] = DYV[kk][0][q];                                                  \
+                    f8[4 + q] = DYV[kk][1][q];                                              \
+                }                                                                           \
+                *reinterpret_cast<half8*>(dyl + fl * a.dy_stride + ohl * a.WC8 + 8 * m) =   \
+                    pack8(f8);                                                              \
+            }                                                                               \
+        }                                                                                   \
+        if (xit >= 0) {                                                                     \
+            const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;              \
+            half_t* const dst = xb2 + ((J) & 1) * x_stage + cl * a.x_plane + row * a.xrow;  \
+            const int plane = 32 * a.x_plane;                                               \
+            const int xc0 = ow0 * a.sw - a.pw;                                              \
+            const int valid_cols = a.Wo - ow0;                                              \
+            if (valid_cols >= a.WC8) {                                                      \
+                switch (xc0 - floor4(xc0)) { /* uniform across the block */                 \
+                    case 0: write_shifts<0, 0, SW, XI::OCT>(XW, a.S, grp, dst, plane); break; \
+                    case 1: write_shifts<1, 0, SW, XI::OCT>(XW, a.S, grp, dst, plane); break; \
+                    case 2: write_shifts<2, 0, SW, XI::OCT>(XW, a.S, grp, dst, plane); break; \
+                    default: write_shifts<3, 0, SW, XI::OCT>(XW, a.S, grp, dst, plane); break; \
+                }                                                                           \
+            } else {                                                                        \
+                /* Edge tile: columns past the output width get 0 (their dY is */          \
+                /* zero; this keeps 0 * inf from turning into NaN). */                      \
+                switch (xc0 - floor4(xc0)) {                                                \
+                    case 0: write_shifts_edge<0, 0, SW, XI::OCT>(XW, a.S, grp, valid_cols, dst, plane); break; \
+                    case 1: write_shifts_edge<1, 0, SW, XI::OCT>(XW, a.S, grp, valid_cols, dst, plane); break; \
+                    case 2: write_shifts_edge<2, 0, SW, XI::OCT>(XW, a.S, grp, valid_cols, dst, plane); break; \
+                    default: write_shifts_edge<3, 0, SW, XI::OCT>(XW, a.S, grp, valid_cols, dst, plane); break; \
+                }                                                                           \
+            }                                                                               \
+        }                                                                                   \
     }
+    // Issue the global loads of step J into DYV/XW.
+#define SEERA_WG_LOAD(J, DYV, XW)                                                           \
+    {                                                                                       \
+        const int item = it0 + (J) / NCH, ch = (J) % NCH;                                   \
+        const int b = tile_b(item), oh0 = tile_oh0(item), ow0 = tile_ow0(item);             \
+        if (ch == 0) {                                                                      \
+            _Pragma("unroll") for (int kk = 0; kk < kWgDyMax; ++kk) {                       \
+                const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16; \
+                const int oh = oh0 + ohl, ow = ow0 + 8 * m;                                 \
+                const bool ok = dyit[kk] >= 0 && fl < f_lim && oh < a.Ho;                   \
+                const float* src =                                                          \
+                    a.dy + (((int64_t)b * a.F + ftile * 64 + fl) * a.Ho + oh) * a.Wo + ow;  \
+                _Pragma("unroll") for (int h = 0; h < 2; ++h) {                             \
+                    DYV[kk][h] = floatx4{0.f, 0.f, 0.f, 0.f};                               \
+                    if (ok && ow + 4 * h < a.Wo)                                            \
+                        DYV[kk][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);        \
+                }                                                                           \
+            }                                                                               \
+        }                                                                                   \
+        if (xit >= 0) {                                                                     \
+            const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;              \
+            const int c = ctile * a.CT + ch * 32 + cl, hin = oh0 * a.sh - a.ph + row;       \
+            const int a0 = floor4(ow0 * a.sw - a.pw) + 8 * XI::OCT * grp * SW;              \
+            const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;                    \
+            const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;            \
+            _Pragma("unroll") for (int q = 0; q < 11; ++q) {                                \
+                const int col = a0 + 4 * q;                                                 \
+                floatx4 x4 = {0.f, 0.f, 0.f, 0.f};                                          \
+                if (q < XI::F4 && rowok && (unsigned)col < (unsigned)a.W)                   \
+                    x4 = *reinterpret_cast<const floatx4*>(src + col);                      \
+                _Pragma("unroll") for (int e = 0; e < 4; ++e) XW[4 * q + e] = x4[e];        \
+            }                                                                               \
+        }                                                                                   \
+    }
+
+    // Steps 0 and 1 in flight, then per step j: write j, load j+2 into the
+    // registers j just freed, and meet the consumers at the barrier that
+    // releases step j to them.
+    if (nsteps > 0) SEERA_WG_LOAD(0, dyv0, xw0)
+    if (nsteps > 1) SEERA_WG_LOAD(1, dyv1, xw1)
+    for (int j = 0; j < nsteps; j += 2) {
+        SEERA_WG_WRITE(j, dyv0, xw0)
+        if (j + 2 < nsteps) SEERA_WG_LOAD(j + 2, dyv0, xw0)
+        __syncthreads();
+        if (j + 1 < nsteps) {
+            SEERA_WG_WRITE(j + 1, dyv1, xw1)
+            if (j + 3 < nsteps) SEERA_WG_LOAD(j + 3, dyv1, xw1)
+            __syncthreads();
+        }
+    }
+#undef SEERA_WG_WRITE
+#undef SEERA_WG_LOAD
     if (nsteps == 0) return;
     __syncthreads();  // matches the consumers' final barrier
 }
@@ -674,9 +686,16 @@ hipError_t launch_wgrad_sw(const WgradArgs& a, int ngw, hipStream_t st) {
         case 3: k = reinterpret_cast<const void*>(band_wgrad_kernel<3, SW, NCH>); break;
         case 4: k = reinterpret_cast<const void*>(band_wgrad_kernel<4, SW, NCH>); break;
         case 5: k = reinterpret_cast<const void*>(band_wgrad_kernel<5, SW, NCH>); break;
-        case 6: k = reinterpret_cast<const void*>(band_wgrad_kernel<6, SW, NCH>); break;
-        case 7: k = reinterpret_cast<const void*>(band_wgrad_kernel<7, SW, NCH>); break;
-        default: k = reinterpret_cast<const void*>(band_wgrad_kernel<8, SW, NCH>); break;
+        default:
+            // Two-chunk tiles are planned only for R*S <= 9 (at most 5 groups).
+            if constexpr (NCH == 1) {
+                if (ngw == 6) k = reinterpret_cast<const void*>(band_wgrad_kernel<6, SW, NCH>);
+                else if (ngw == 7) k = reinterpret_cast<const void*>(band_wgrad_kernel<7, SW, NCH>);
+                else k = reinterpret_cast<const void*>(band_wgrad_kernel<8, SW, NCH>);
+            } else {
+                return hipErrorInvalidValue;
+            }
+            break;
     }
     if (a.lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
