@@ -208,6 +208,19 @@ def cpu_baseline(n=4096, reps=5):
     }
 
 
+def copy_calibration(nbytes, reps=3):
+    """Device-to-device copies of a known size (the runtime's copy kernel):
+    the reference point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE
+    counters to bytes (each copy reads and writes nbytes)."""
+    lib = capi.load()
+    src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+    capi.check(lib.seera_hip_memset(src.ptr, 0, nbytes))
+    for _ in range(reps):
+        capi.check(lib.seera_hip_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+    capi.check(lib.seera_hip_synchronize())
+    print(f"copy calibration: {reps} device-to-device copies of {nbytes} bytes", flush=True)
+
+
 def traffic_from_profiles():
     """HBM bytes per GEMM launch measured with rocprofv3 --pmc (committed
     summary under profiles/), or None if not measured."""
@@ -227,6 +240,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run device copies of BYTES (counter calibration), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU "
@@ -236,6 +251,9 @@ def main():
     if not capi.gpu_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     stream = Stream()
     n = 4096
