@@ -81,6 +81,19 @@ struct WgradArgs {
     int64_t lds_bytes;
 };
 
+// Per-block partial sums of dW written by stream_wgrad_partials
+// (conv_wgrad.hip): part[tile][split][64 f][CT*R*S], column (r*S + s)*CT + c.
+struct WgradPartials {
+    float* part;
+    int CT, nctile, ntiles, nsplit;
+};
+
+// Row-streaming dW partials of a stride-1 convolution (R, S <= 3, rows
+// float4-aligned); *used reports whether it ran. The caller reduces them.
+int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,
+                          int R, int S, int ph, int pw, hipStream_t st, WgradPartials* out,
+                          bool* used);
+
 // dW [F, C, R, S] = sum over (b, oh, ow) of dY[b, f, oh, ow] *
 // X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies.
 int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,

@@ -812,6 +812,20 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
                     int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used) {
     *used = false;
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    if (sh == 1 && sw == 1) {
+        WgradPartials wp{};
+        bool streamed = false;
+        SEERA_TRY(stream_wgrad_partials(Y, X, B, C, H, W, F, R, S, ph, pw, st, &wp, &streamed));
+        if (streamed) {
+            const int64_t total = (int64_t)wp.ntiles * 64 * wp.CT * R * S;
+            hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
+                               dim3(kRedCols * kRedGroups), 0, st, wp.part, dW, F, C, R, S, wp.CT,
+                               wp.nctile, wp.ntiles, wp.nsplit);
+            SEERA_HIP_TRY(hipGetLastError());
+            *used = true;
+            return SEERA_OK;
+        }
+    }
     if (Wo % 4 != 0 || W % 4 != 0 || sw > 2 || S > 7 || R * S > 18 || !aligned16(Y) ||
         !aligned16(X) || B == 0)
         return SEERA_OK;

@@ -1,0 +1,356 @@
+// conv_wgrad.hip -- row-streaming weight gradient of a stride-1 convolution.
+//
+//   dW[f, c, r, s] = sum_{b, oh, ow} dY[b, f, oh, ow] * X[b, c, oh - ph + r, ow - pw + s]
+// (convolution.cu:268-366, 431-452): a GEMM with M = filters, N = (tap,
+// channel), K = output pixels. A block owns one image, a strip of L output
+// rows, 64 filters and 64 channels, and keeps the whole 64 x (64*R*S) partial
+// in registers while it walks the strip two output rows per step:
+//   * 4 producer waves stream the dY rows of the step and the X rows the step
+//     adds (fp16, pixel-contiguous per channel, as in HBM) into two LDS rings,
+//     loading two steps ahead;
+//   * 8 consumer waves, one per (half of the filters, 16 channels), run
+//     v_mfma_f32_16x16x32_f16 with 16 filters x 32 pixels of dY as A and 16
+//     channels x 32 pixels of X as B. The S column taps of an X row are one
+//     aligned 16-byte read plus the next two pixels, shifted in registers
+//     (v_alignbit), so the ring holds each X row once.
+// Each block writes its partial; wgrad_reduce (conv_band.hip) adds them in a
+// fixed order. HBM sees each dY element once and each X row once per strip
+// plus R-1 halo rows.
+#include "conv_band.h"
+#include "mfma_core.h"
+
+namespace seera {
+namespace {
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+constexpr int kG = 2;            // output rows per step
+constexpr int kCons = 512;       // 8 consumer waves
+constexpr int kProd = 256;       // 4 producer waves
+constexpr int kNT = kCons + kProd;
+constexpr int kXI = 5;           // X items (1 channel x 8 pixels) per producer thread per step
+constexpr int kDI = 4;           // dY items per producer thread per step
+constexpr int kTile = 64;        // filters and channels per block
+
+struct WStreamArgs {
+    const float* dy;     // [B, F, Ho, Wo]
+    const float* x;      // [B, C, H, W]
+    float* part;         // [tiles][nsplit][64][64*R*S]
+    int B, C, H, W, F, Ho, Wo, R, S, ph, pw;
+    int L, nstrip, nsplit, nctile;
+    int Wp;              // padded row length (pixels, multiple of 32)
+    int rs;              // LDS row stride in halves (Wp + 8: an odd number of 16-byte slots)
+    int NR;              // X ring rows (2*kG + R - 1)
+    int64_t lds_bytes;
+};
+
+// Funnel shift of the 8 halves in b by one half, pulling in the low half of n.
+__device__ __forceinline__ half8 shift1(half8 b, uint32_t n) {
+    const uintx4_t u = __builtin_bit_cast(uintx4_t, b);
+    uintx4_t o;
+    o[0] = __builtin_amdgcn_alignbit(u[1], u[0], 16);
+    o[1] = __builtin_amdgcn_alignbit(u[2], u[1], 16);
+    o[2] = __builtin_amdgcn_alignbit(u[3], u[2], 16);
+    o[3] = __builtin_amdgcn_alignbit(n, u[3], 16);
+    return __builtin_bit_cast(half8, o);
+}
+// ... by two halves (one dword).
+__device__ __forceinline__ half8 shift2(half8 b, uint32_t n) {
+    const uintx4_t u = __builtin_bit_cast(uintx4_t, b);
+    uintx4_t o;
+    o[0] = u[1];
+    o[1] = u[2];
+    o[2] = u[3];
+    o[3] = n;
+    return __builtin_bit_cast(half8, o);
+}
+
+// 8 consecutive floats starting D floats into the 12-float window w0|w1|w2.
+template <int D>
+__device__ __forceinline__ half8 pick8(floatx4 w0, floatx4 w1, floatx4 w2) {
+    float v[12] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = v[D + i];
+    return pack8(o);
+}
+
+template <int RR, int SS>
+__global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    const int split = blockIdx.x, ty = blockIdx.y;
+    const int b = split / a.nstrip, strip = split - b * a.nstrip;
+    const int ftile = ty / a.nctile, ctile = ty - ftile * a.nctile;
+    const int ohA = strip * a.L;
+    const int Lb = min(a.L, a.Ho - ohA);         // output rows of this strip
+    const int nsteps = (Lb + kG - 1) / kG;
+    const int xplane = kTile * a.rs;             // halves per X ring row
+    half_t* const xr = smem;                     // [NR][64 c][rs]
+    half_t* const dr = smem + a.NR * xplane;     // [2*kG][64 f][rs]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    if (wave < kCons / 64) {
+        // ---- consumers ----
+        const int fh = wave & 1, cg = wave >> 1;
+        const int kc = lane >> 4;
+        // Fragment offsets within a ring row: dY rows f = 32*fh + 16*fg + lane%16,
+        // X rows c = 16*cg + lane%16, pixels 8*kc..8*kc+7 of a 32-pixel block.
+        const int aoff = (32 * fh + (lane & 15)) * a.rs + 8 * kc;
+        const int boff = (16 * cg + (lane & 15)) * a.rs + 8 * kc;
+        floatx4_t acc[2][RR][SS];
+#pragma unroll
+        for (int fg = 0; fg < 2; ++fg)
+#pragma unroll
+            for (int r = 0; r < RR; ++r)
+#pragma unroll
+                for (int s = 0; s < SS; ++s) acc[fg][r][s] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        const int nkb = a.Wp >> 5;
+        for (int st = 0; st < nsteps; ++st) {
+            __syncthreads();  // the rows of step st are in the rings
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                const int o = st * kG + g;       // output row (strip-relative)
+                if (o >= Lb) continue;
+                const half_t* const dl = dr + (o % (2 * kG)) * (kTile * a.rs) + aoff;
+                for (int kb = 0; kb < nkb; ++kb) {
+                    half8 fa[2];
+#pragma unroll
+                    for (int fg = 0; fg < 2; ++fg)
+                        fa[fg] = *reinterpret_cast<const half8*>(dl + fg * 16 * a.rs + kb * 32);
+#pragma unroll
+                    for (int r = 0; r < RR; ++r) {
+                        int slot = o + r;
+                        slot = slot >= a.NR ? slot % a.NR : slot;
+                        const half_t* const xl = xr + slot * xplane + boff + kb * 32;
+                        const half8 base = *reinterpret_cast<const half8*>(xl);
+                        const uint32_t nb = *reinterpret_cast<const uint32_t*>(xl + 8);
+                        half8 fb[SS];
+                        fb[0] = base;
+                        if constexpr (SS > 1) fb[1] = shift1(base, nb);
+                        if constexpr (SS > 2) fb[2] = shift2(base, nb);
+#pragma unroll
+                        for (int s = 0; s < SS; ++s)
+#pragma unroll
+                            for (int fg = 0; fg < 2; ++fg)
+                                acc[fg][r][s] = mfma16x16x32(fa[fg], fb[s], acc[fg][r][s]);
+                    }
+                }
+            }
+        }
+        // Partial: part[ty][split][f64][n], n = (r*S + s)*64 + c; lane holds
+        // filters 4*(lane/16) + i at channel lane%16 of its 16x16 tile.
+        const int ntot = kTile * RR * SS;
+        float* const dst = a.part + ((int64_t)ty * a.nsplit + split) * 64 * ntot;
+#pragma unroll
+        for (int fg = 0; fg < 2; ++fg)
+#pragma unroll
+            for (int r = 0; r < RR; ++r)
+#pragma unroll
+                for (int s = 0; s < SS; ++s) {
+                    const int n = (r * SS + s) * kTile + 16 * cg + (lane & 15);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        dst[(int64_t)(32 * fh + 16 * fg + 4 * kc + i) * ntot + n] = acc[fg][r][s][i];
+                }
+        return;
+    }
+
+    // ---- producers ----
+    // X item (row of the group, channel, octet j): ring columns 8j..8j+7 hold
+    // X[.., ih, 8j - pw .. 8j - pw + 7]; loaded as three aligned float4s from
+    // column 8j - pw - dd and picked at offset dd (dd uniform). dY item (row,
+    // filter, octet j): columns 8j..8j+7 of the dY row (zero past Wo).
+    // Buffer resources over this image's tile planes: out-of-range rows,
+    // columns, channels and filters read 0.
+    const int ptid = tid - kCons;
+    const int c0 = ctile * kTile, f0 = ftile * kTile;
+    const rsrc_t xsrc = make_rsrc(a.x + ((int64_t)b * a.C + c0) * a.H * a.W);
+    const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + f0) * a.Ho * a.Wo);
+    const int nxo = a.rs >> 3;                   // X octets per ring row (Wp/8 + 1)
+    const int ndo = a.Wp >> 3;                   // dY octets per ring row
+    const int dd = ((-a.pw) % 4 + 4) % 4;
+    const int need = Lb + RR - 1;                // strip-relative X rows used
+    const int ih0 = ohA - a.ph;                  // image row of strip X row 0
+    int xrow[kXI], xch[kXI], xcol[kXI];          // row in group (kG: none), channel, first column (aligned)
+#pragma unroll
+    for (int k = 0; k < kXI; ++k) {
+        const int it = ptid + k * kProd;
+        const int j = it % nxo, rest = it / nxo;
+        xch[k] = rest % kTile;
+        xrow[k] = it < kG * kTile * nxo ? rest / kTile : kG;
+        xcol[k] = 8 * j - a.pw - dd;
+    }
+    int drow[kDI], dfl[kDI], dcol[kDI];
+#pragma unroll
+    for (int k = 0; k < kDI; ++k) {
+        const int it = ptid + k * kProd;
+        const int j = it % ndo, rest = it / ndo;
+        dfl[k] = rest % kTile;
+        drow[k] = it < kG * kTile * ndo ? rest / kTile : kG;
+        dcol[k] = 8 * j;
+    }
+    floatx4 xv[kXI][3], dv[kDI][2];
+
+    // Loads of X group rows [I0, I0 + NX) and dY output rows [O0, O0 + ND).
+#define SEERA_WG_LOAD(I0, NX, O0, ND)                                                      \
+    {                                                                                      \
+        _Pragma("unroll") for (int k = 0; k < kXI; ++k) {                                  \
+            const int i = (I0) + xrow[k], ih = ih0 + i;                                    \
+            const bool rok = xrow[k] < (NX) && (unsigned)i < (unsigned)need &&             \
+                             (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C;            \
+            _Pragma("unroll") for (int q = 0; q < 3; ++q) {                                \
+                const int col = xcol[k] + 4 * q;                                           \
+                const uint32_t off = rok && (unsigned)col < (unsigned)a.W                  \
+                    ? (uint32_t)(((xch[k] * a.H + ih) * a.W + col) * 4) : kBufOOB;         \
+                xv[k][q] = buf_load4(xsrc, off);                                           \
+            }                                                                              \
+        }                                                                                  \
+        _Pragma("unroll") for (int k = 0; k < kDI; ++k) {                                  \
+            const int o = (O0) + drow[k];                                                  \
+            const bool rok = drow[k] < (ND) && o < Lb && f0 + dfl[k] < a.F;                \
+            _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                \
+                const int col = dcol[k] + 4 * q;                                           \
+                const uint32_t off = rok && col < a.Wo                                     \
+                    ? (uint32_t)(((dfl[k] * a.Ho + ohA + o) * a.Wo + col) * 4) : kBufOOB;  \
+                dv[k][q] = buf_load4(dsrc, off);                                           \
+            }                                                                              \
+        }                                                                                  \
+    }
+    // Round and write them into the rings.
+#define SEERA_WG_STORE(I0, NX, O0, ND)                                                     \
+    {                                                                                      \
+        _Pragma("unroll") for (int k = 0; k < kXI; ++k) {                                  \
+            const int i = (I0) + xrow[k];                                                  \
+            if (xrow[k] < (NX) && (unsigned)i < (unsigned)need) {                          \
+                half8 h;                                                                   \
+                switch (dd) {                                                              \
+                    case 0: h = pick8<0>(xv[k][0], xv[k][1], xv[k][2]); break;             \
+                    case 1: h = pick8<1>(xv[k][0], xv[k][1], xv[k][2]); break;             \
+                    case 2: h = pick8<2>(xv[k][0], xv[k][1], xv[k][2]); break;             \
+                    default: h = pick8<3>(xv[k][0], xv[k][1], xv[k][2]); break;            \
+                }                                                                          \
+                *reinterpret_cast<half8*>(xr + (i % a.NR) * xplane + xch[k] * a.rs +       \
+                                          xcol[k] + a.pw + dd) = h;                        \
+            }                                                                              \
+        }                                                                                  \
+        _Pragma("unroll") for (int k = 0; k < kDI; ++k) {                                  \
+            const int o = (O0) + drow[k];                                                  \
+            if (drow[k] < (ND) && o < Lb) {                                                \
+                float v8[8];                                                               \
+                _Pragma("unroll") for (int q = 0; q < 4; ++q) {                            \
+                    v8[q] = dv[k][0][q];                                                   \
+                    v8[4 + q] = dv[k][1][q];                                               \
+                }                                                                          \
+                *reinterpret_cast<half8*>(dr + (o % (2 * kG)) * (kTile * a.rs) +           \
+                                          dfl[k] * a.rs + dcol[k]) = pack8(v8);            \
+            }                                                                              \
+        }                                                                                  \
+    }
+    // Strip X row i sits in ring slot i % NR; the X rows step g adds are
+    // [RR-1 + g*kG, RR-1 + (g+1)*kG), after RR-1 halo rows.
+    if (RR > 1) {
+        SEERA_WG_LOAD(0, RR - 1, 0, 0)
+        SEERA_WG_STORE(0, RR - 1, 0, 0)
+    }
+    SEERA_WG_LOAD(RR - 1, kG, 0, kG)
+    SEERA_WG_STORE(RR - 1, kG, 0, kG)
+    SEERA_WG_LOAD(RR - 1 + kG, kG, kG, kG)
+    __syncthreads();  // releases step 0
+    for (int st = 0; st + 1 < nsteps; ++st) {
+        // The slots written now held rows only step st-1 read.
+        SEERA_WG_STORE(RR - 1 + (st + 1) * kG, kG, (st + 1) * kG, kG)
+        SEERA_WG_LOAD(RR - 1 + (st + 2) * kG, kG, (st + 2) * kG, kG)
+        __syncthreads();  // releases step st+1
+    }
+#undef SEERA_WG_LOAD
+#undef SEERA_WG_STORE
+}
+
+template <int RR>
+hipError_t launch_rr(const WStreamArgs& a, int ntiles, hipStream_t st) {
+    const void* k;
+    switch (a.S) {
+        case 1: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 1>); break;
+        case 2: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 2>); break;
+        default: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 3>); break;
+    }
+    hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)a.lds_bytes);
+    if (e != hipSuccess) return e;
+    void* args[] = {const_cast<WStreamArgs*>(&a)};
+    return hipLaunchKernel(k, dim3(a.nsplit, ntiles), dim3(kNT), args, (size_t)a.lds_bytes, st);
+}
+
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
+}  // namespace
+
+int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,
+                          int R, int S, int ph, int pw, hipStream_t st, WgradPartials* out,
+                          bool* used) {
+    *used = false;
+    const int Ho = H + 2 * ph - R + 1, Wo = W + 2 * pw - S + 1;
+    if (R < 1 || R > 3 || S < 1 || S > 3 || Ho <= 0 || Wo <= 0 || B <= 0) return SEERA_OK;
+    if (W % 4 != 0 || Wo % 4 != 0 || ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y)) & 15))
+        return SEERA_OK;
+    WStreamArgs a{};
+    a.dy = Y; a.x = X;
+    a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Ho = Ho; a.Wo = Wo;
+    a.R = R; a.S = S; a.ph = ph; a.pw = pw;
+    a.Wp = (Wo + 31) & ~31;
+    a.rs = a.Wp + 8;
+    a.NR = 2 * kG + R - 1;
+    // Columns read: 8*j - pw (j < rs/8) must cover every X column an output
+    // pixel reads, Wo - 1 - pw + S - 1 < Wp + 8 - pw: true since S <= 3.
+    const int nxo = a.rs / 8, ndo = a.Wp / 8;
+    if (kG * kTile * nxo > kProd * kXI || kG * kTile * ndo > kProd * kDI ||
+        (R - 1) * kTile * nxo > kProd * kXI)
+        return SEERA_OK;
+    a.lds_bytes = (int64_t)(a.NR + 2 * kG) * kTile * a.rs * 2;
+    if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
+    const int64_t img = (int64_t)kTile * H * W * 4, dimg = (int64_t)kTile * Ho * Wo * 4;
+    if (img > kMaxTileSpanBytes || dimg > kMaxTileSpanBytes) return SEERA_OK;
+    a.nctile = (C + kTile - 1) / kTile;
+    const int ntiles = a.nctile * ((F + kTile - 1) / kTile);
+    // Strip length: fewest rounds of one block per CU, each about (steps + 2)
+    // step times (the first rows arrive unhidden).
+    const int ncu = device_cus();
+    double best = 1e30;
+    for (int L = kG; L < Ho + kG; L += kG) {
+        const int64_t blocks = (int64_t)B * ((Ho + L - 1) / L) * ntiles;
+        const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + kG - 1) / kG + 2);
+        if (cost < best) { best = cost; a.L = L; }
+    }
+    a.nstrip = (Ho + a.L - 1) / a.L;
+    a.nsplit = B * a.nstrip;
+    void* ws = nullptr;
+    SEERA_TRY(workspace(sizeof(float) * (size_t)ntiles * a.nsplit * 64 * kTile * R * S, &ws));
+    a.part = static_cast<float*>(ws);
+    hipError_t e;
+    switch (R) {
+        case 1: e = launch_rr<1>(a, ntiles, st); break;
+        case 2: e = launch_rr<2>(a, ntiles, st); break;
+        default: e = launch_rr<3>(a, ntiles, st); break;
+    }
+    if (e != hipSuccess) return fail_hip(e, "stream wgrad launch");
+    out->part = a.part;
+    out->CT = kTile;
+    out->nctile = a.nctile;
+    out->ntiles = ntiles;
+    out->nsplit = a.nsplit;
+    *used = true;
+    return SEERA_OK;
+}
+
+}  // namespace seera
