@@ -5,7 +5,7 @@
 // channel), K = output pixels. A block owns one image, a strip of L output
 // rows, 64 filters and 64 channels, and keeps the whole 64 x (64*R*S) partial
 // in registers while it walks the strip two output rows per step:
-//   * 4 producer waves stream the dY rows of the step and the X rows the step
+//   * 8 producer waves stream the dY rows of the step and the X rows the step
 //     adds (fp16, pixel-contiguous per channel, as in HBM) into two LDS rings,
 //     loading two steps ahead;
 //   * 8 consumer waves, one per (half of the filters, 16 channels), run
@@ -31,10 +31,10 @@ __device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c)
 
 constexpr int kG = 2;            // output rows per step
 constexpr int kCons = 512;       // 8 consumer waves
-constexpr int kProd = 256;       // 4 producer waves
+constexpr int kProd = 512;       // 8 producer waves
 constexpr int kNT = kCons + kProd;
-constexpr int kXI = 5;           // X items (1 channel x 8 pixels) per producer thread per step
-constexpr int kDI = 4;           // dY items per producer thread per step
+constexpr int kXI = 3;           // X items (1 channel x 8 pixels) per producer thread per step
+constexpr int kDI = 2;           // dY items per producer thread per step
 constexpr int kTile = 64;        // filters and channels per block
 
 struct WStreamArgs {
