@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
 #pragma unroll
             for (int k = 0; k < kWBatch; ++k) {
                 const int i = i0 + k * kNT + tid;
-                if (i < n16) lds_write8<32>(wl + (i >> 8) * 2048, (i & 255) >> 2, i & 3, wv[k]);
+                if (i < n16)
+                    *reinterpret_cast<half8*>(wl + (i >> 8) * 2048 + ring_off((i & 255) >> 2, i & 3)) = wv[k];
             }
         }
     }
@@ -137,14 +138,14 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     if (wave < 2 * kG) {
         // ---- consumers: one half output row per step ----
         const int kc = lane >> 4;                // k chunk of this lane's fragments
-        // Weight fragment offsets (tap 0, chunk 0): groups 2 and 3 sit 1024
-        // halves past groups 0 and 1 under lds_off<32> (the swizzle depends on
-        // the group's parity only).
+        // Weight fragment offsets (tap 0, chunk 0). The 64 x 32 weight slice
+        // of a tap uses the ring's pixel layout (filter f in place of pixel p),
+        // which serves this 16-row x 2-chunk read pattern without bank
+        // conflicts (the GEMM tile swizzle lds_off<32> would cost 2x here);
+        // filter group fg sits 512*fg halves further.
         int wrow[4];
-        wrow[0] = lds_off<32>(lane & 15, kc);
-        wrow[1] = lds_off<32>(16 + (lane & 15), kc);
-        wrow[2] = wrow[0] + 1024;
-        wrow[3] = wrow[1] + 1024;
+#pragma unroll
+        for (int fg = 0; fg < 4; ++fg) wrow[fg] = ring_off(lane & 15, kc) + 512 * fg;
         const int nqt = a.nchunks * taps;
         // Output: buffer resource over this image's [F, Hout, Wout] block;
         // lanes outside the tile get kBufOOB and their stores are dropped.

@@ -44,7 +44,7 @@ struct WStreamArgs {
     int B, C, H, W, F, Ho, Wo, R, S, ph, pw;
     int L, nstrip, nsplit, nctile;
     int Wp;              // padded row length (pixels, multiple of 32)
-    int rs;              // LDS row stride in halves (Wp + 8: an odd number of 16-byte slots)
+    int rs;              // LDS row stride in halves (Wp + 16: 2 mod 4 16-byte slots)
     int NR;              // X ring rows (2*kG + R - 1)
     int64_t lds_bytes;
 };
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     const int c0 = ctile * kTile, f0 = ftile * kTile;
     const rsrc_t xsrc = make_rsrc(a.x + ((int64_t)b * a.C + c0) * a.H * a.W);
     const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + f0) * a.Ho * a.Wo);
-    const int nxo = a.rs >> 3;                   // X octets per ring row (Wp/8 + 1)
+    const int nxo = (a.Wp >> 3) + 1;             // X octets per ring row
     const int ndo = a.Wp >> 3;                   // dY octets per ring row
     const int dd = ((-a.pw) % 4 + 4) % 4;
     const int need = Lb + RR - 1;                // strip-relative X rows used
@@ -309,11 +309,14 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Ho = Ho; a.Wo = Wo;
     a.R = R; a.S = S; a.ph = ph; a.pw = pw;
     a.Wp = (Wo + 31) & ~31;
-    a.rs = a.Wp + 8;
+    // Row stride Wp + 16 halves (2 mod 4 slots of 16 bytes): the fragment
+    // reads (16 rows x 4 column chunks per wave) measured free of LDS bank
+    // conflicts at that stride and 2-way conflicted at Wp + 8.
+    a.rs = a.Wp + 16;
     a.NR = 2 * kG + R - 1;
-    // Columns read: 8*j - pw (j < rs/8) must cover every X column an output
-    // pixel reads, Wo - 1 - pw + S - 1 < Wp + 8 - pw: true since S <= 3.
-    const int nxo = a.rs / 8, ndo = a.Wp / 8;
+    // X octets per row: columns up to Wp + 7 (the last 32-pixel block's
+    // fragments plus the two pixels the column taps shift in).
+    const int nxo = a.Wp / 8 + 1, ndo = a.Wp / 8;
     if (kG * kTile * nxo > kProd * kXI || kG * kTile * ndo > kProd * kDI ||
         (R - 1) * kTile * nxo > kProd * kXI)
         return SEERA_OK;
