@@ -39,6 +39,21 @@ CONV2D = [
     ("big_s2", 8, 32, 64, 64, 64, 3, 3, 2, 1),
 ]
 
+# Shapes that exercise the row-streaming kernels' tiling (not from the
+# reference's tests): several and partial 64-channel / 64-filter tiles,
+# 3 input-channel chunks, 5x5 taps, rows that are not a multiple of 16
+# pixels, two column tiles, a strip split, odd padding.
+CONV2D_STREAM = [
+    ("s01", 2, 96, 20, 20, 80, 3, 3, 1, 1),    # 2 F tiles (64+16), 2 C tiles for dW, 3 chunks
+    ("s02", 3, 16, 24, 24, 24, 5, 5, 1, 2),    # 5x5 forward / dX stream, dW band path
+    ("s03", 2, 8, 30, 60, 16, 3, 3, 1, 1),     # 60-pixel rows
+    ("s04", 1, 32, 12, 100, 32, 3, 3, 1, 1),   # 2 column tiles (52 + 48)
+    ("s05", 2, 24, 64, 32, 40, 3, 3, 1, 1),    # long strips
+    ("s06", 2, 16, 16, 16, 16, 3, 3, 1, 0),    # no padding (output 14x14 -> dX stream needs ph=2)
+    ("s07", 2, 16, 17, 16, 16, 2, 2, 1, 1),    # even kernel, 18x17 output
+    ("s08", 4, 64, 16, 16, 64, 1, 1, 1, 0),    # 1x1: a GEMM over pixels
+]
+
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
 CONVT = [
     ("t01", 2, 4, 4, 4, 8, 3, 3, 1, 0),
