@@ -23,10 +23,9 @@
 //     to fp16, channel-last) into the ring and issue the loads of step s+2.
 // The ring holds 2*4 + T - 1 rows, so one barrier per step suffices, and the
 // consumers never wait on the input loads nor the producers on the output
-// stores. The weights are loaded once per block, ahead of any input row,
-// and stay resident; every input row is read
-// from HBM once per strip (plus T-1 halo rows), so HBM sees each input and
-// output element about once.
+// stores. The weights are loaded once per block, ahead of any input row, and
+// stay resident; every input row is read from HBM once per strip (plus T-1
+// halo rows), so HBM sees each input and output element about once.
 #include "conv_band.h"
 #include "mfma_core.h"
 
@@ -56,7 +55,8 @@ constexpr int kCons = 2 * kG * 64; // consumer threads (two waves per row)
 constexpr int kProd = 256;         // producer threads
 constexpr int kNT = kCons + kProd;
 constexpr int kItems = 2;          // input items per producer thread per step
-constexpr int kWBatch = 6;         // weight pieces per thread per batch
+constexpr int kPreW = 12;          // weight pieces (16 B) per thread, prologue
+constexpr int kPreItems = 2;       // input items per thread, prologue
 constexpr int kTailPad = 1024;     // LDS bytes past the ring (reads of padding lanes)
 
 struct StreamArgs {
@@ -78,7 +78,8 @@ struct StreamArgs {
     BandPhase ph[kBandMaxPhases];  // nrb = strips, ncb = column tiles
 };
 
-template <int PXG>
+// UC: every phase has 3 column taps (0: any).
+template <int PXG, int UC>
 __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int bx = blockIdx.x;
@@ -115,22 +116,67 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     // wave (output row, ring slots) stay wave-uniform in SGPRs.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // ---- weights, by all waves, before any input row is requested ----
+    // ---- prologue, by all waves: the weights and the first T-1+kG input
+    // rows (halo and group 0) are requested at once, then written to LDS;
+    // the producers then request group 1 and release step 0 ----
     {
         const half_t* wsrc = a.wk + P.woff + (int64_t)ftile * a.nchunks * taps * 2048;
-        const int n16 = a.nchunks * taps * 256;
-        for (int i0 = 0; i0 < n16; i0 += kNT * kWBatch) {
-            half8 wv[kWBatch];
+        const int n16 = a.nchunks * taps * 256;  // <= kPreW * kNT (host check)
+        half8 wv[kPreW];
 #pragma unroll
-            for (int k = 0; k < kWBatch; ++k) {
-                const int i = i0 + k * kNT + tid;
-                if (i < n16) wv[k] = *reinterpret_cast<const half8*>(wsrc + (int64_t)i * 8);
-            }
+        for (int k = 0; k < kPreW; ++k) {
+            const int i = k * kNT + tid;
+            if (i < n16) wv[k] = *reinterpret_cast<const half8*>(wsrc + (int64_t)i * 8);
+        }
+        // Items as the producers' (row, chunk, 8-channel group cg, column
+        // quad q4), cg fastest, over strip input rows [-sh, g0 + kG).
+        const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+        const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
+        const int row_items = a.nchunks * 4 * nq;
+        const int nitems = (g0 + sh + kG) * row_items;  // <= kPreItems * kNT (host check)
+        const int need = Lb + T - 1;
+        floatx4 xv[kPreItems][8];
 #pragma unroll
-            for (int k = 0; k < kWBatch; ++k) {
-                const int i = i0 + k * kNT + tid;
-                if (i < n16)
-                    *reinterpret_cast<half8*>(wl + (i >> 8) * 2048 + ring_off((i & 255) >> 2, i & 3)) = wv[k];
+        for (int k = 0; k < kPreItems; ++k) {
+            const int it = k * kNT + tid;
+            const int cg = it & 3;
+            int r = it >> 2;
+            const int q4 = r % nq;
+            r /= nq;
+            const int ch = r % a.nchunks;
+            const int i = r / a.nchunks - sh;        // strip input row
+            const int hin = ohA - P.iph + i;
+            const int c0 = ch * 32 + cg * 8, win = ic0 + q4 * 4;
+            const bool ok = it < nitems && (unsigned)i < (unsigned)need &&
+                            (unsigned)hin < (unsigned)a.H && c0 < a.C && (unsigned)win < (unsigned)a.W;
+            const uint32_t vo = ok ? (uint32_t)((c0 * a.H * a.W + hin * a.W + win) * 4) : kBufOOB;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xv[k][j] = buf_load4s(src, vo, j * cstride);
+        }
+#pragma unroll
+        for (int k = 0; k < kPreW; ++k) {
+            const int i = k * kNT + tid;
+            if (i < n16)
+                *reinterpret_cast<half8*>(wl + (i >> 8) * 2048 + ring_off((i & 255) >> 2, i & 3)) = wv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kPreItems; ++k) {
+            const int it = k * kNT + tid;
+            const int cg = it & 3;
+            int r = it >> 2;
+            const int q4 = r % nq;
+            r /= nq;
+            const int ch = r % a.nchunks;
+            const int i = r / a.nchunks - sh;
+            if (it < nitems && (unsigned)i < (unsigned)need) {
+                half_t* dst = ring + (i % a.NR) * a.nchunks * plane + ch * plane + q4 * 128;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float col[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) col[j] = xv[k][j][q];
+                    *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + q, cg) - 4 * q4 * 32) = pack8(col);
+                }
             }
         }
     }
@@ -153,10 +199,39 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         const int hw = a.Hout * a.Wout;
         const int fl = ftile * 64 + (lane & 15);  // filter of this lane (+ fg*16)
         const int px0 = (wave / kG) * PXG * 16;   // first pixel of this wave's half row
+        // Pixel fragment offsets within a ring plane per column tap (UC == 3).
+        int poff[UC == 3 ? 3 : 1][PXG];
+        if constexpr (UC == 3) {
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+#pragma unroll
+                for (int pg = 0; pg < PXG; ++pg)
+                    poff[u][pg] = ring_off(px0 + pg * 16 + (lane & 15) + u + coff, kc);
+        }
+        // UC == 3: a step's results wait in res (byte offsets roff, kBufOOB:
+        // none) and are stored between the MFMA blocks of the next step, so
+        // the output stores overlap the MFMAs instead of stalling the wave
+        // at the end of every step while the memory pipe drains.
+        floatx4_t res[UC == 3 ? PXG : 1][4];
+        uint32_t roff[UC == 3 ? PXG : 1][4];
+        bool pending = false;
+#define SEERA_STREAM_FLUSH(PG, FG0)                                                         \
+    _Pragma("unroll") for (int fg = (FG0); fg < (FG0) + 2; ++fg)                            \
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, res[PG][fg]),   \
+                                               dst_img, roff[PG][fg], 0, 0);
         for (int s = 0; s < nsteps; ++s) {
             __syncthreads();  // the rows of step s are in the ring
             const int o = s * kG + wave % kG - sh;  // output row of this wave (strip-relative)
-            if (o < 0 || o >= Lb || px0 >= a.WC) continue;
+            if (o < 0 || o >= Lb || px0 >= a.WC) {
+                if constexpr (UC == 3) {
+                    if (pending) {
+#pragma unroll
+                        for (int pg = 0; pg < PXG; ++pg) { SEERA_STREAM_FLUSH(pg, 0) SEERA_STREAM_FLUSH(pg, 2) }
+                        pending = false;
+                    }
+                }
+                continue;
+            }
             // acc[pg][fg]: pixels of group pg (rows) x filters of group fg
             // (columns); lane holds pixels 4*(lane/16) + r at filter lane%16.
             floatx4_t acc[PXG][4];
@@ -190,14 +265,70 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     _Pragma("unroll") for (int pg = 0; pg < PXG; ++pg)                                      \
         _Pragma("unroll") for (int fg = 0; fg < 4; ++fg)                                    \
             acc[pg][fg] = mfma16x16x32(fb[BUF][pg], fa[BUF][fg], acc[pg][fg]);
-            // Reads run one fragment set ahead of the MFMAs and are issued
-            // unconditionally, so every MFMA waits only for its own set.
-            SEERA_STREAM_READ(0)
-            for (int q = 0; q < nqt; q += 2) {
-                SEERA_STREAM_READ(1)
-                SEERA_STREAM_MMA(0)
+            if constexpr (UC == 3) {
+                // Three column taps known at compile time: the sets of one
+                // (chunk, row tap) pair use fragment buffers 0, 1, 2 and reads
+                // run two sets ahead of the MFMAs (one set ahead leaves the
+                // MFMAs waiting on LDS latency with 8 waves reading). Pixel
+                // offsets per tap are per-lane constants, weight offsets are
+                // immediates off one base per pair.
+                const int nct = a.nchunks * T;
+                int ct_t = 0, ct_ch = 0;  // (row tap, chunk) of the pair being read
+#define SEERA_STREAM_READ3(T_, CH_, U_, BUF)                                                \
+    {                                                                                       \
+        const half_t* w = wl + ((CH_) * T + (T_)) * 6144 + (U_) * 2048;                     \
+        int slot = slot0 + (T_);                                                            \
+        if (slot >= a.NR) slot -= a.NR;                                                     \
+        const half_t* rp = ring + (slot * a.nchunks + (CH_)) * plane;                       \
+        _Pragma("unroll") for (int pg = 0; pg < PXG; ++pg) fb3[BUF][pg] =                   \
+            *reinterpret_cast<const half8*>(rp + poff[U_][pg]);                             \
+        _Pragma("unroll") for (int fg = 0; fg < 4; ++fg) fa3[BUF][fg] =                     \
+            *reinterpret_cast<const half8*>(w + wrow[fg]);                                  \
+    }
+#define SEERA_STREAM_MMA3(BUF)                                                              \
+    _Pragma("unroll") for (int pg = 0; pg < PXG; ++pg)                                      \
+        _Pragma("unroll") for (int fg = 0; fg < 4; ++fg)                                    \
+            acc[pg][fg] = mfma16x16x32(fb3[BUF][pg], fa3[BUF][fg], acc[pg][fg]);
+                half8 fa3[3][4], fb3[3][PXG];
+                SEERA_STREAM_READ3(0, 0, 0, 0)
+                SEERA_STREAM_READ3(0, 0, 1, 1)
+                for (int ct = 0; ct < nct; ++ct) {
+                    SEERA_STREAM_READ3(ct_t, ct_ch, 2, 2)
+                    // the next pair (the last one again past the end)
+                    if (ct + 1 < nct) {
+                        if (++ct_t == T) { ct_t = 0; ++ct_ch; }
+                    }
+                    SEERA_STREAM_MMA3(0)
+                    // the previous step's results: pixel group ct (ct < PXG)
+                    if (pending && ct < PXG) {
+                        if (ct == 0) { SEERA_STREAM_FLUSH(0, 0) }
+                        if (PXG > 1 && ct == 1) { SEERA_STREAM_FLUSH(PXG - 1, 0) }
+                    }
+                    SEERA_STREAM_READ3(ct_t, ct_ch, 0, 0)
+                    SEERA_STREAM_MMA3(1)
+                    if (pending && ct < PXG) {
+                        if (ct == 0) { SEERA_STREAM_FLUSH(0, 2) }
+                        if (PXG > 1 && ct == 1) { SEERA_STREAM_FLUSH(PXG - 1, 2) }
+                    }
+                    SEERA_STREAM_READ3(ct_t, ct_ch, 1, 1)
+                    SEERA_STREAM_MMA3(2)
+                }
+                if (pending && PXG > 1 && nct < 2) {
+                    SEERA_STREAM_FLUSH(PXG - 1, 0)
+                    SEERA_STREAM_FLUSH(PXG - 1, 2)
+                }
+#undef SEERA_STREAM_READ3
+#undef SEERA_STREAM_MMA3
+            } else {
+                // Reads run one fragment set ahead of the MFMAs and are issued
+                // unconditionally, so every MFMA waits only for its own set.
                 SEERA_STREAM_READ(0)
-                if (q + 1 < nqt) { SEERA_STREAM_MMA(1) }
+                for (int q = 0; q < nqt; q += 2) {
+                    SEERA_STREAM_READ(1)
+                    SEERA_STREAM_MMA(0)
+                    SEERA_STREAM_READ(0)
+                    if (q + 1 < nqt) { SEERA_STREAM_MMA(1) }
+                }
             }
 #undef SEERA_STREAM_READ
 #undef SEERA_STREAM_MMA
@@ -213,11 +344,24 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
                     const int f = fl + fg * 16;
                     const uint32_t off =
                         pok && f < a.F ? (uint32_t)((f * hw + orow + ow0 + px) * 4) : kBufOOB;
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        __builtin_bit_cast(uintx4_t, acc[pg][fg]), dst_img, off, 0, 0);
+                    if constexpr (UC == 3) {
+                        res[pg][fg] = acc[pg][fg];
+                        roff[pg][fg] = off;
+                    } else {
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(uintx4_t, acc[pg][fg]), dst_img, off, 0, 0);
+                    }
                 }
             }
+            pending = UC == 3;
         }
+        if constexpr (UC == 3) {
+            if (pending) {
+#pragma unroll
+                for (int pg = 0; pg < PXG; ++pg) { SEERA_STREAM_FLUSH(pg, 0) SEERA_STREAM_FLUSH(pg, 2) }
+            }
+        }
+#undef SEERA_STREAM_FLUSH
         return;
     }
 
@@ -259,7 +403,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     floatx4 v[kItems][8];  // one step's items: 8 channels x 4 columns each
 
     // Issue the loads of the rows [I0, I0 + NROWS) that this thread's items cover.
-#define SEERA_STREAM_LOAD(I0, NROWS)                                                        \
+#define SEERA_STREAM_LOAD(V, I0, NROWS)                                                     \
     {                                                                                       \
         _Pragma("unroll") for (int k = 0; k < kItems; ++k) {                                \
             const int i = (I0) + prow[k];                                                   \
@@ -268,11 +412,11 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
                             (unsigned)hin < (unsigned)a.H && pcol[k] != kBufOOB;            \
             const uint32_t vo = ok ? pcol[k] + (uint32_t)(hin * a.W * 4) : kBufOOB;         \
             _Pragma("unroll") for (int j = 0; j < 8; ++j)                                   \
-                v[k][j] = buf_load4s(src, vo, j * cstride);                                 \
+                V[k][j] = buf_load4s(src, vo, j * cstride);                                 \
         }                                                                                   \
     }
     // Round the loaded items to fp16 and write them into their ring slots.
-#define SEERA_STREAM_STORE(I0, NROWS)                                                       \
+#define SEERA_STREAM_STORE(V, I0, NROWS)                                                    \
     {                                                                                       \
         _Pragma("unroll") for (int k = 0; k < kItems; ++k) {                                \
             const int i = (I0) + prow[k];                                                   \
@@ -280,7 +424,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
                 half_t* dst = ring + (i % a.NR) * a.nchunks * plane + pdst[k];              \
                 _Pragma("unroll") for (int q = 0; q < 4; ++q) {                             \
                     float col[8];                                                           \
-                    _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = v[k][j][q];      \
+                    _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = V[k][j][q];      \
                     /* = ring_off(4*q4 + q, cg) relative to pixel 4*q4 */                   \
                     *reinterpret_cast<half8*>(dst + q * 32 +                                \
                                               ((pcg[k] ^ ((prq[k] + (q >> 1)) & 3)) << 3)) = \
@@ -289,25 +433,23 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
             }                                                                               \
         }                                                                                   \
     }
-    SEERA_STREAM_LOAD(-sh, T - 1)
-    SEERA_STREAM_STORE(-sh, T - 1)
-    SEERA_STREAM_LOAD(g0, kG)
-    SEERA_STREAM_STORE(g0, kG)
-    SEERA_STREAM_LOAD(g0 + kG, kG)
-    __syncthreads();  // releases step 0
+    __syncthreads();  // releases step 0 (the prologue wrote its rows)
+    // Group 1 is requested after the release: issued before it, these loads
+    // wait behind every block's prologue traffic and hold step 0 back.
+    SEERA_STREAM_LOAD(v, g0 + kG, kG)
     for (int s = 0; s + 1 < nsteps; ++s) {
         // Ring slots of group s+1 held the rows only step s-1 read.
-        SEERA_STREAM_STORE(g0 + (s + 1) * kG, kG)
-        SEERA_STREAM_LOAD(g0 + (s + 2) * kG, kG)
+        SEERA_STREAM_STORE(v, g0 + (s + 1) * kG, kG)
+        SEERA_STREAM_LOAD(v, g0 + (s + 2) * kG, kG)
         __syncthreads();  // releases step s+1
     }
 #undef SEERA_STREAM_LOAD
 #undef SEERA_STREAM_STORE
 }
 
-template <int PXG>
+template <int PXG, int UC>
 hipError_t launch_pxg(const StreamArgs& a, int nftiles, hipStream_t st) {
-    auto kern = stream_conv_kernel<PXG>;
+    auto kern = stream_conv_kernel<PXG, UC>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)a.lds_bytes);
@@ -362,6 +504,10 @@ int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     for (int z = 0; z < a.nphase; ++z)
         if (a.ph[z].opw != 0 || a.ph[z].oph != 0) return SEERA_OK;
     if (kG * a.nchunks * a.BC4 > kProd * kItems) return SEERA_OK;  // items per step
+    // prologue: weight pieces and the first T-1+kG rows' items per thread
+    if (a.nchunks * max_taps * 256 > kPreW * kNT ||
+        (max_t - 1 + kG) * a.nchunks * a.BC4 > kPreItems * kNT)
+        return SEERA_OK;
     // Strip length: fewest rounds of one block per CU, each costing about
     // (steps + 1.5) step times (the prologue fetches the first rows unhidden).
     const int ncu = device_cus();
@@ -389,10 +535,12 @@ int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     if (a.nblocks == 0 || nftiles == 0) { *used = true; return SEERA_OK; }
     const int pxg = ((a.WC + 15) / 16 + 1) / 2;  // pixel groups per consumer wave
     hipError_t e;
-    switch (pxg) {
-        case 1: e = launch_pxg<1>(a, nftiles, st); break;
-        default: e = launch_pxg<2>(a, nftiles, st); break;
-    }
+    bool u3 = true;
+    for (int z = 0; z < a.nphase; ++z) u3 = u3 && a.ph[z].U == 3;
+    if (u3)
+        e = pxg == 1 ? launch_pxg<1, 3>(a, nftiles, st) : launch_pxg<2, 3>(a, nftiles, st);
+    else
+        e = pxg == 1 ? launch_pxg<1, 0>(a, nftiles, st) : launch_pxg<2, 0>(a, nftiles, st);
     if (e != hipSuccess) return fail_hip(e, "stream conv launch");
     *used = true;
     return SEERA_OK;
