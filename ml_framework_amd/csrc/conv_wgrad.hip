@@ -113,35 +113,60 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         const int nkb = a.Wp >> 5;
         for (int st = 0; st < nsteps; ++st) {
             __syncthreads();  // the rows of step st are in the rings
+            // The step's (row g, 32-pixel block kb) pairs q = g*nkb + kb. The
+            // LDS reads run one tap row ahead of the MFMAs (the last tap row
+            // of pair q reads pair q+1's dY fragments and first X row), and
+            // are issued unconditionally: past the last pair they re-read it.
+            const int nq = min(kG, Lb - st * kG) * nkb;
+            int gn = 0, kbn = 0;  // pair whose fragments are read next
+            const half_t* dln = dr + ((st * kG) % (2 * kG)) * (kTile * a.rs) + aoff;
+            half8 fan[2], xbn;
+            uint32_t xnn;
+#define SEERA_WG_READ_A()                                                                  \
+    {                                                                                      \
+        _Pragma("unroll") for (int fg = 0; fg < 2; ++fg) fan[fg] =                         \
+            *reinterpret_cast<const half8*>(dln + fg * 16 * a.rs + kbn * 32);              \
+    }
+#define SEERA_WG_READ_X(R_)                                                                \
+    {                                                                                      \
+        int slot = st * kG + gn + (R_);                                                    \
+        slot = slot >= a.NR ? slot % a.NR : slot;                                          \
+        const half_t* const xl = xr + slot * xplane + boff + kbn * 32;                     \
+        xbn = *reinterpret_cast<const half8*>(xl);                                         \
+        xnn = *reinterpret_cast<const uint32_t*>(xl + 8);                                  \
+    }
+            SEERA_WG_READ_A()
+            SEERA_WG_READ_X(0)
+            for (int q = 0; q < nq; ++q) {
+                const half8 fa[2] = {fan[0], fan[1]};
 #pragma unroll
-            for (int g = 0; g < kG; ++g) {
-                const int o = st * kG + g;       // output row (strip-relative)
-                if (o >= Lb) continue;
-                const half_t* const dl = dr + (o % (2 * kG)) * (kTile * a.rs) + aoff;
-                for (int kb = 0; kb < nkb; ++kb) {
-                    half8 fa[2];
-#pragma unroll
-                    for (int fg = 0; fg < 2; ++fg)
-                        fa[fg] = *reinterpret_cast<const half8*>(dl + fg * 16 * a.rs + kb * 32);
-#pragma unroll
-                    for (int r = 0; r < RR; ++r) {
-                        int slot = o + r;
-                        slot = slot >= a.NR ? slot % a.NR : slot;
-                        const half_t* const xl = xr + slot * xplane + boff + kb * 32;
-                        const half8 base = *reinterpret_cast<const half8*>(xl);
-                        const uint32_t nb = *reinterpret_cast<const uint32_t*>(xl + 8);
-                        half8 fb[SS];
-                        fb[0] = base;
-                        if constexpr (SS > 1) fb[1] = shift1(base, nb);
-                        if constexpr (SS > 2) fb[2] = shift2(base, nb);
-#pragma unroll
-                        for (int s = 0; s < SS; ++s)
-#pragma unroll
-                            for (int fg = 0; fg < 2; ++fg)
-                                acc[fg][r][s] = mfma16x16x32(fa[fg], fb[s], acc[fg][r][s]);
+                for (int r = 0; r < RR; ++r) {
+                    const half8 base = xbn;
+                    const uint32_t nb = xnn;
+                    if (r + 1 < RR) {
+                        SEERA_WG_READ_X(r + 1)
+                    } else {
+                        if (q + 1 < nq && ++kbn == nkb) {
+                            kbn = 0;
+                            ++gn;
+                            dln = dr + ((st * kG + gn) % (2 * kG)) * (kTile * a.rs) + aoff;
+                        }
+                        SEERA_WG_READ_A()
+                        SEERA_WG_READ_X(0)
                     }
+                    half8 fb[SS];
+                    fb[0] = base;
+                    if constexpr (SS > 1) fb[1] = shift1(base, nb);
+                    if constexpr (SS > 2) fb[2] = shift2(base, nb);
+#pragma unroll
+                    for (int s = 0; s < SS; ++s)
+#pragma unroll
+                        for (int fg = 0; fg < 2; ++fg)
+                            acc[fg][r][s] = mfma16x16x32(fa[fg], fb[s], acc[fg][r][s]);
                 }
             }
+#undef SEERA_WG_READ_A
+#undef SEERA_WG_READ_X
         }
         // Partial: part[ty][split][f64][n], n = (r*S + s)*64 + c; lane holds
         // filters 4*(lane/16) + i at channel lane%16 of its 16x16 tile.
