@@ -211,15 +211,28 @@ __global__ void prep_fwd_weights(const float* __restrict__ W, half_t* __restrict
     wk[i] = to_half(v);
 }
 
-// Wk for one stride phase of the transposed convolution (conv dX): the
-// band kernel's output channel is the conv input channel c (< Cc), its input
-// channel is the conv output channel f (< Fc); tap (t, u) of the phase reads
-// W[f, c, r0h + sh*(T-1-t), r0w + sw*(U-1-u)] (W is [Fc, Cc, R, S]).
+// Tap geometry of the stride phases of a dX weight preparation: phase z's
+// prepared weights are halves [begin[z], begin[z+1]) of Wk, in phase order.
+struct DgradPrepPhases {
+    int nphase;
+    int64_t begin[kBandMaxPhases + 1];
+    int T[kBandMaxPhases], U[kBandMaxPhases], r0h[kBandMaxPhases], r0w[kBandMaxPhases];
+};
+
+// Wk for the stride phases of the transposed convolution (conv dX), all
+// phases in one launch: the band kernel's output channel is the conv input
+// channel c (< Cc), its input channel is the conv output channel f (< Fc);
+// tap (t, u) of phase z reads W[f, c, r0h + sh*(T-1-t), r0w + sw*(U-1-u)]
+// (W is [Fc, Cc, R, S]).
 __global__ void prep_dgrad_weights(const float* __restrict__ W, half_t* __restrict__ wk, int Fc,
-                                   int Cc, int R, int S, int sh, int sw, int r0h, int r0w, int T,
-                                   int U, int nchunks, int64_t total) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
+                                   int Cc, int R, int S, int sh, int sw, int nchunks,
+                                   const DgradPrepPhases pp) {
+    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= pp.begin[pp.nphase]) return;
+    int z = 0;
+    while (z + 1 < pp.nphase && gi >= pp.begin[z + 1]) ++z;
+    const int64_t i = gi - pp.begin[z];
+    const int T = pp.T[z], U = pp.U[z];
     const int k32 = (int)(i & 31), o64 = (int)((i >> 5) & 63);
     int64_t rest = i >> 11;
     const int taps = T * U;
@@ -230,10 +243,10 @@ __global__ void prep_dgrad_weights(const float* __restrict__ W, half_t* __restri
     const int c = otile * 64 + o64;   // conv input channel = band output channel
     const int f = chunk * 32 + k32;   // conv output channel = band input channel
     const int t = tap / U, u = tap - t * U;
-    const int r = r0h + sh * (T - 1 - t), s = r0w + sw * (U - 1 - u);
+    const int r = pp.r0h[z] + sh * (T - 1 - t), s = pp.r0w[z] + sw * (U - 1 - u);
     float v = 0.f;
     if (c < Cc && f < Fc) v = W[(((int64_t)f * Cc + c) * R + r) * S + s];
-    wk[i] = to_half(v);
+    wk[gi] = to_half(v);
 }
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
@@ -792,12 +805,20 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(half_t) * (size_t)std::max<int64_t>(woff, 1), &ws));
     a.wk = static_cast<const half_t*>(ws);
-    for (int z = 0; z < a.nphase; ++z) {
-        const int64_t n = (int64_t)a.nftiles * a.nchunks * a.ph[z].T * a.ph[z].U * 2048;
-        if (n == 0) continue;
-        hipLaunchKernelGGL(prep_dgrad_weights, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           Wconv, static_cast<half_t*>(ws) + a.ph[z].woff, Fc, Cc, R, S, sh, sw,
-                           ax[z][0].r0, ax[z][1].r0, a.ph[z].T, a.ph[z].U, a.nchunks, n);
+    if (woff > 0) {
+        // One launch for every phase's weights (they sit back to back in ws).
+        DgradPrepPhases pp{};
+        pp.nphase = a.nphase;
+        for (int z = 0; z < a.nphase; ++z) {
+            pp.begin[z] = a.ph[z].woff;
+            pp.T[z] = a.ph[z].T;
+            pp.U[z] = a.ph[z].U;
+            pp.r0h[z] = ax[z][0].r0;
+            pp.r0w[z] = ax[z][1].r0;
+        }
+        pp.begin[a.nphase] = woff;
+        hipLaunchKernelGGL(prep_dgrad_weights, dim3((unsigned)((woff + 255) / 256)), dim3(256), 0,
+                           st, Wconv, static_cast<half_t*>(ws), Fc, Cc, R, S, sh, sw, a.nchunks, pp);
         SEERA_HIP_TRY(hipGetLastError());
     }
     bool streamed = false;
