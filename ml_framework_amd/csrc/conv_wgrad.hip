@@ -80,7 +80,8 @@ __device__ __forceinline__ half8 pick8(floatx4 w0, floatx4 w1, floatx4 w2) {
     return pack8(o);
 }
 
-template <int RR, int SS>
+// DD: the column misalignment (-pw) mod 4 when known at compile time (-1: any).
+template <int RR, int SS, int DD>
 __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int split = blockIdx.x, ty = blockIdx.y;
@@ -199,10 +200,13 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + f0) * a.Ho * a.Wo);
     const int nxo = (a.Wp >> 3) + 1;             // X octets per ring row
     const int ndo = a.Wp >> 3;                   // dY octets per ring row
-    const int dd = ((-a.pw) % 4 + 4) % 4;
+    const int dd = DD >= 0 ? DD : ((-a.pw) % 4 + 4) % 4;
     const int need = Lb + RR - 1;                // strip-relative X rows used
     const int ih0 = ohA - a.ph;                  // image row of strip X row 0
-    int xrow[kXI], xch[kXI], xcol[kXI];          // row in group (kG: none), channel, first column (aligned)
+    // Per X item: row in group (kG: none), channel, first column (aligned),
+    // byte offset of (channel, group row, first column) in the image tile, and
+    // which of its three column quads lie inside the image.
+    int xrow[kXI], xch[kXI], xcol[kXI], xoff[kXI], xqm[kXI];
 #pragma unroll
     for (int k = 0; k < kXI; ++k) {
         const int it = ptid + k * kProd;
@@ -210,8 +214,12 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         xch[k] = rest % kTile;
         xrow[k] = it < kG * kTile * nxo ? rest / kTile : kG;
         xcol[k] = 8 * j - a.pw - dd;
+        xoff[k] = ((xch[k] * a.H + xrow[k]) * a.W + xcol[k]) * 4;
+        xqm[k] = 0;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) xqm[k] |= (unsigned)(xcol[k] + 4 * q) < (unsigned)a.W ? 1 << q : 0;
     }
-    int drow[kDI], dfl[kDI], dcol[kDI];
+    int drow[kDI], dfl[kDI], dcol[kDI], doff[kDI], dqm[kDI];
 #pragma unroll
     for (int k = 0; k < kDI; ++k) {
         const int it = ptid + k * kProd;
@@ -219,30 +227,32 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         dfl[k] = rest % kTile;
         drow[k] = it < kG * kTile * ndo ? rest / kTile : kG;
         dcol[k] = 8 * j;
+        doff[k] = ((dfl[k] * a.Ho + ohA + drow[k]) * a.Wo + dcol[k]) * 4;
+        dqm[k] = (dcol[k] < a.Wo ? 1 : 0) | (dcol[k] + 4 < a.Wo ? 2 : 0);
     }
     floatx4 xv[kXI][3], dv[kDI][2];
 
     // Loads of X group rows [I0, I0 + NX) and dY output rows [O0, O0 + ND).
 #define SEERA_WG_LOAD(I0, NX, O0, ND)                                                      \
     {                                                                                      \
+        const int xrb = (ih0 + (I0)) * a.W * 4;  /* image row of group row 0, in bytes */  \
         _Pragma("unroll") for (int k = 0; k < kXI; ++k) {                                  \
             const int i = (I0) + xrow[k], ih = ih0 + i;                                    \
             const bool rok = xrow[k] < (NX) && (unsigned)i < (unsigned)need &&             \
                              (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C;            \
             _Pragma("unroll") for (int q = 0; q < 3; ++q) {                                \
-                const int col = xcol[k] + 4 * q;                                           \
-                const uint32_t off = rok && (unsigned)col < (unsigned)a.W                  \
-                    ? (uint32_t)(((xch[k] * a.H + ih) * a.W + col) * 4) : kBufOOB;         \
+                const uint32_t off = rok && ((xqm[k] >> q) & 1)                            \
+                    ? (uint32_t)(xoff[k] + xrb + 16 * q) : kBufOOB;                        \
                 xv[k][q] = buf_load4(xsrc, off);                                           \
             }                                                                              \
         }                                                                                  \
+        const int drb = (O0) * a.Wo * 4;                                                   \
         _Pragma("unroll") for (int k = 0; k < kDI; ++k) {                                  \
             const int o = (O0) + drow[k];                                                  \
             const bool rok = drow[k] < (ND) && o < Lb && f0 + dfl[k] < a.F;                \
             _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                \
-                const int col = dcol[k] + 4 * q;                                           \
-                const uint32_t off = rok && col < a.Wo                                     \
-                    ? (uint32_t)(((dfl[k] * a.Ho + ohA + o) * a.Wo + col) * 4) : kBufOOB;  \
+                const uint32_t off = rok && ((dqm[k] >> q) & 1)                            \
+                    ? (uint32_t)(doff[k] + drb + 16 * q) : kBufOOB;                        \
                 dv[k][q] = buf_load4(dsrc, off);                                           \
             }                                                                              \
         }                                                                                  \
@@ -250,17 +260,24 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     // Round and write them into the rings.
 #define SEERA_WG_STORE(I0, NX, O0, ND)                                                     \
     {                                                                                      \
+        const int xs0 = (I0) % a.NR;  /* ring slot of group row 0 (uniform) */             \
         _Pragma("unroll") for (int k = 0; k < kXI; ++k) {                                  \
             const int i = (I0) + xrow[k];                                                  \
+            int slot = xs0 + xrow[k];                                                      \
+            slot = slot >= a.NR ? slot - a.NR : slot;                                      \
             if (xrow[k] < (NX) && (unsigned)i < (unsigned)need) {                          \
                 half8 h;                                                                   \
-                switch (dd) {                                                              \
-                    case 0: h = pick8<0>(xv[k][0], xv[k][1], xv[k][2]); break;             \
-                    case 1: h = pick8<1>(xv[k][0], xv[k][1], xv[k][2]); break;             \
-                    case 2: h = pick8<2>(xv[k][0], xv[k][1], xv[k][2]); break;             \
-                    default: h = pick8<3>(xv[k][0], xv[k][1], xv[k][2]); break;            \
+                if constexpr (DD >= 0) {                                                   \
+                    h = pick8<DD < 0 ? 0 : DD>(xv[k][0], xv[k][1], xv[k][2]);              \
+                } else {                                                                   \
+                    switch (dd) {                                                          \
+                        case 0: h = pick8<0>(xv[k][0], xv[k][1], xv[k][2]); break;         \
+                        case 1: h = pick8<1>(xv[k][0], xv[k][1], xv[k][2]); break;         \
+                        case 2: h = pick8<2>(xv[k][0], xv[k][1], xv[k][2]); break;         \
+                        default: h = pick8<3>(xv[k][0], xv[k][1], xv[k][2]); break;        \
+                    }                                                                      \
                 }                                                                          \
-                *reinterpret_cast<half8*>(xr + (i % a.NR) * xplane + xch[k] * a.rs +       \
+                *reinterpret_cast<half8*>(xr + slot * xplane + xch[k] * a.rs +             \
                                           xcol[k] + a.pw + dd) = h;                        \
             }                                                                              \
         }                                                                                  \
@@ -300,10 +317,17 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
 template <int RR>
 hipError_t launch_rr(const WStreamArgs& a, int ntiles, hipStream_t st) {
     const void* k;
+    // 3x3 with pad 0 or 1 (column misalignment 0 or 3) gets the misalignment
+    // at compile time; other shapes pick it at run time.
+    const int dd = ((-a.pw) % 4 + 4) % 4;
     switch (a.S) {
-        case 1: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 1>); break;
-        case 2: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 2>); break;
-        default: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 3>); break;
+        case 1: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 1, -1>); break;
+        case 2: k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 2, -1>); break;
+        default:
+            if (RR == 3 && dd == 3) k = reinterpret_cast<const void*>(stream_wgrad_kernel<3, 3, 3>);
+            else if (RR == 3 && dd == 0) k = reinterpret_cast<const void*>(stream_wgrad_kernel<3, 3, 0>);
+            else k = reinterpret_cast<const void*>(stream_wgrad_kernel<RR, 3, -1>);
+            break;
     }
     hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)a.lds_bytes);
     if (e != hipSuccess) return e;
