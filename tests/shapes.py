@@ -52,6 +52,8 @@ CONV2D_STREAM = [
     ("s06", 2, 16, 16, 16, 16, 3, 3, 1, 0),    # no padding (output 14x14 -> dX stream needs ph=2)
     ("s07", 2, 16, 17, 16, 16, 2, 2, 1, 1),    # even kernel, 18x17 output
     ("s08", 4, 64, 16, 16, 64, 1, 1, 1, 0),    # 1x1: a GEMM over pixels
+    ("s09", 2, 16, 8, 64, 16, 1, 3, 1, 1),     # 1x3, one chunk: a single (chunk, row tap) pair, 2 pixel groups
+    ("s10", 2, 8, 6, 16, 8, 1, 3, 1, 1),       # 1x3, one chunk, 1 pixel group
 ]
 
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
