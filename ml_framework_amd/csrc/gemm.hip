@@ -49,6 +49,21 @@ struct GemmProblem {
     __device__ __forceinline__ void load_b(S& s, int n0, int k0, int k1, int tid) const {
         s.load(B, ldb, n0, N, k0, k1, tid);
     }
+    // Streaming stagers for the large warp-specialised tile (vector loads only).
+    static constexpr bool kWsStream = VA == 4 && VB == 4;
+    template <int R, int BK, int NP>
+    using WA = typename std::conditional<A_KC, WsStageKC<R, BK, NP>, WsStageMNC<R, BK, NP>>::type;
+    template <int R, int BK, int NP>
+    using WB = typename std::conditional<B_KC, WsStageKC<R, BK, NP>, WsStageMNC<R, BK, NP>>::type;
+    template <class S>
+    __device__ __forceinline__ void ws_init_a(S& s, int m0, int tid) const {
+        s.init(A, lda, m0, M, tid);
+    }
+    template <class S>
+    __device__ __forceinline__ void ws_init_b(S& s, int n0, int tid) const {
+        s.init(B, ldb, n0, N, tid);
+    }
+
     template <class S>
     __device__ __forceinline__ void init_a(S&, int, int) const {}
     template <class S>

@@ -140,10 +140,45 @@ struct WsCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS tile exceeds the 160 KB of a gfx950 CU");
 };
 
+// Consumer side of the warp-specialised kernels: one barrier per slice, then
+// the slice's MFMAs from LDS stage kt&1; finally the accumulators are stored.
+template <int BM, int BN, int BK, int CWM, int CWN, class P>
+__device__ __forceinline__ void ws_consume(const P& p, const half_t* smem, int m0, int n0, int nk,
+                                           int wave, int lane) {
+    constexpr int TM = BM / CWM / 32, TN = BN / CWN / 32;
+    constexpr int STAGE = (BM + BN) * BK;
+    const int wm0 = (wave / CWN) * (BM / CWM), wn0 = (wave % CWN) * (BN / CWN);
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int kt = 0; kt < nk; ++kt) {
+        __syncthreads();  // slice kt is in stage kt&1
+        const half_t* const now = smem + (kt & 1) * STAGE;
+        mfma_slice<BK, TM, TN, false>(now, now + BM * BK, wm0, wn0, lane, acc);
+    }
+    const int z = blockIdx.z;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.M) p.store(m, n, z, acc[i][j][r]);
+            }
+    }
+}
+
 template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>
 __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const P p) {
     using Cfg = WsCfg<BM, BN, BK, CWM, CWN, NPW>;
-    constexpr int TM = Cfg::TM, TN = Cfg::TN, NC = Cfg::NC, NP = Cfg::NP;
+    constexpr int NC = Cfg::NC, NP = Cfg::NP;
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     constexpr int STAGE = (BM + BN) * BK;
 
@@ -156,32 +191,7 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     if (tid < NC) {
-        const int wm0 = (wave / CWN) * (BM / CWM), wn0 = (wave % CWN) * (BN / CWN);
-        floatx16 acc[TM][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-        for (int kt = 0; kt < nk; ++kt) {
-            __syncthreads();  // slice kt is in stage kt&1
-            const half_t* const now = smem + (kt & 1) * STAGE;
-            mfma_slice<BK, TM, TN, false>(now, now + BM * BK, wm0, wn0, lane, acc);
-        }
-        const int z = blockIdx.z;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn0 + j * 32 + (lane & 31);
-            if (n >= p.N) continue;
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (m < p.M) p.store(m, n, z, acc[i][j][r]);
-                }
-        }
+        ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
         return;
     }
 
@@ -220,6 +230,126 @@ hipError_t launch_igemm_ws(const P& p, int splits, hipStream_t stream) {
     const int tiles_m = (p.M + BM - 1) / BM;
     dim3 grid(tiles_m * p.tiles_n, 1, splits);
     auto kern = igemm_ws_kernel<BM, BN, BK, CWM, CWN, NPW, P>;
+    if (Cfg::LDS_BYTES > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Cfg::LDS_BYTES);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), Cfg::LDS_BYTES, stream, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Warp-specialised kernel with streaming producers, for problems that supply
+// streaming stagers (P::template WA / WB, p.ws_init_a / ws_init_b) and whose
+// K range per split is a whole number of BK slices (checked by the host). Same
+// consumers and the same LDS image as igemm_ws_kernel; the producers keep two
+// K slices of loads in flight (register sets 0 and 1) and, part by part, round
+// slice t+1 into LDS and at once reuse that part's registers for the loads of
+// slice t+3. Loads past the last slice re-read it (never stored), so the load
+// count per step is fixed and the compiler's vmcnt waits stay exact.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>
+__global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws2_kernel(const P p) {
+    using Cfg = WsCfg<BM, BN, BK, CWM, CWN, NPW>;
+    constexpr int NC = Cfg::NC, NP = Cfg::NP;
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    constexpr int STAGE = (BM + BN) * BK;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, p.tiles_n, p.gm, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = blockIdx.z * p.k_split;
+    const int kend = min(p.K, kbeg + p.k_split);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    if (tid < NC) {
+        ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
+        return;
+    }
+    if (nk == 0) return;
+
+    const int ptid = tid - NC;
+    using SA = typename P::template WA<BM, BK, NP>;
+    using SB = typename P::template WB<BN, BK, NP>;
+    SA sa;
+    SB sb;
+    p.ws_init_a(sa, m0, ptid);
+    p.ws_init_b(sb, n0, ptid);
+    typename SA::Regs ra[2];
+    typename SB::Regs rb[2];
+    auto kof = [&](int s) { return kbeg + min(s, nk - 1) * BK; };
+
+    // The sched barriers pin the issue order (A parts, then B parts, each
+    // store followed by the loads that reuse its registers); the prologue
+    // issues in the same order as the loop so that the waits stay exact.
+#define SEERA_WS_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define SEERA_WS_LOADS(S, s)                                                   \
+    do {                                                                       \
+        const int k0_ = kof(s);                                                \
+        const rsrc_t xa_ = sa.slice(k0_), xb_ = sb.slice(k0_);                 \
+        _Pragma("unroll") for (int q = 0; q < SA::PARTS; ++q) {                \
+            sa.load(ra[S], q, xa_);                                 \
+            SEERA_WS_FENCE();                                                  \
+        }                                                                      \
+        _Pragma("unroll") for (int q = 0; q < SB::PARTS; ++q) {                \
+            sb.load(rb[S], q, xb_);                                 \
+            SEERA_WS_FENCE();                                                  \
+        }                                                                      \
+    } while (0)
+    // Round slice s (register set S) into LDS stage s&1 and refill set S with
+    // slice s+2.
+#define SEERA_WS_STEP(S, s)                                                    \
+    do {                                                                       \
+        half_t* const st_ = smem + ((s) & 1) * STAGE;                          \
+        const int k0_ = kof((s) + 2);                                          \
+        const rsrc_t xa_ = sa.slice(k0_), xb_ = sb.slice(k0_);                 \
+        _Pragma("unroll") for (int q = 0; q < SA::PARTS; ++q) {                \
+            SEERA_WS_FENCE();                                                  \
+            sa.store(ra[S], q, st_, ptid);                                     \
+            SEERA_WS_FENCE();                                                  \
+            sa.load(ra[S], q, xa_);                                 \
+        }                                                                      \
+        _Pragma("unroll") for (int q = 0; q < SB::PARTS; ++q) {                \
+            SEERA_WS_FENCE();                                                  \
+            sb.store(rb[S], q, st_ + BM * BK, ptid);                           \
+            SEERA_WS_FENCE();                                                  \
+            sb.load(rb[S], q, xb_);                                 \
+        }                                                                      \
+        SEERA_WS_FENCE();                                                      \
+    } while (0)
+
+    SEERA_WS_FENCE();
+    SEERA_WS_LOADS(0, 0);
+    SEERA_WS_LOADS(1, 1);
+    SEERA_WS_STEP(0, 0);
+    __syncthreads();  // releases slice 0
+    int s = 1;
+    for (; s + 1 < nk; s += 2) {
+        SEERA_WS_STEP(1, s);
+        __syncthreads();  // releases slice s
+        SEERA_WS_STEP(0, s + 1);
+        __syncthreads();  // releases slice s+1
+    }
+    if (s < nk) {
+        SEERA_WS_STEP(1, s);
+        __syncthreads();
+    }
+#undef SEERA_WS_STEP
+#undef SEERA_WS_LOADS
+#undef SEERA_WS_FENCE
+    // Drain the (unused) loads still in flight before the wave ends.
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
+template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>
+hipError_t launch_igemm_ws2(const P& p, int splits, hipStream_t stream) {
+    using Cfg = WsCfg<BM, BN, BK, CWM, CWN, NPW>;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    dim3 grid(tiles_m * p.tiles_n, 1, splits);
+    auto kern = igemm_ws2_kernel<BM, BN, BK, CWM, CWN, NPW, P>;
     if (Cfg::LDS_BYTES > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -229,6 +229,99 @@ struct StageMNC {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Streaming stagers for the warp-specialised producers (igemm_ws2_kernel).
+// Same tile, same fp16 LDS image as StageKC / StageMNC with VEC=4, but split
+// so that a producer can overlap its loads with its stores:
+//   init(base, ld, r0, rmax, tid)  per-thread item offsets, once per block
+//   slice(k0)                      buffer resource of the K slice at k0
+//   load(regs, q, rsrc)            issue the loads of part q into `regs`
+//   store(regs, q, tile, tid)      round part q to fp16 and write it to LDS
+// A dead row (>= rmax) keeps an offset past num_records and reads 0. Every K
+// slice is whole (the host sends K % BK != 0 to igemm_ws_kernel): a per-load
+// k predicate costs registers and, under a branch, exact vmcnt waits.
+// ---------------------------------------------------------------------------
+template <int ROWS, int BK, int NP>
+struct WsStageKC {
+    static constexpr int TPR = BK / 8;                // threads per row
+    static constexpr int PARTS = ROWS * TPR / NP;     // rows NP/TPR apart
+    static_assert(ROWS * TPR % NP == 0 && NP % TPR == 0, "tile does not split into parts");
+    struct Regs {
+        floatx4 v[PARTS][2];
+    };
+    const float* base;  // element (r0, 0)
+    uint32_t off[PARTS];
+    int dk;
+
+    __device__ __forceinline__ void init(const float* b, int64_t ld, int r0, int rmax, int tid) {
+        base = b + (int64_t)r0 * ld;
+        dk = (tid % TPR) * 8;
+#pragma unroll
+        for (int q = 0; q < PARTS; ++q) {
+            const int dr = q * (NP / TPR) + tid / TPR;
+            off[q] = r0 + dr < rmax ? (uint32_t)(dr * ld + dk) * 4u : kBufOOB;
+        }
+    }
+    __device__ __forceinline__ rsrc_t slice(int k0) const { return make_rsrc(base + k0); }
+    __device__ __forceinline__ void load(Regs& r, int q, rsrc_t rs) const {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) r.v[q][h] = buf_load4(rs, off[q] + 16u * h);
+    }
+    __device__ __forceinline__ void store(const Regs& r, int q, half_t* tile, int tid) const {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = r.v[q][0][j];
+            v[4 + j] = r.v[q][1][j];
+        }
+        lds_write8<BK>(tile, q * (NP / TPR) + tid / TPR, tid % TPR, pack8(v));
+    }
+};
+
+template <int ROWS, int BK, int NP>
+struct WsStageMNC {
+    static constexpr int CG = ROWS / 4;               // 4-row groups
+    static constexpr int PARTS = CG * (BK / 8) / NP;  // k groups NP/CG apart
+    static_assert(CG * (BK / 8) % NP == 0 && NP % CG == 0, "tile does not split into parts");
+    struct Regs {
+        floatx4 v[PARTS][8];
+    };
+    const float* base;  // element (r0, k = 0)
+    uint32_t off[PARTS];
+    uint32_t kstep;     // bytes between consecutive k
+    int dk[PARTS];
+
+    __device__ __forceinline__ void init(const float* b, int64_t ld, int r0, int rmax, int tid) {
+        base = b + r0;
+        kstep = (uint32_t)ld * 4u;
+        const int dr = (tid % CG) * 4;
+#pragma unroll
+        for (int q = 0; q < PARTS; ++q) {
+            dk[q] = (q * (NP / CG) + tid / CG) * 8;
+            off[q] = r0 + dr < rmax ? (uint32_t)(dk[q] * ld + dr) * 4u : kBufOOB;
+        }
+    }
+    __device__ __forceinline__ rsrc_t slice(int k0) const {
+        return make_rsrc(base + (int64_t)k0 * (kstep / 4u));
+    }
+    __device__ __forceinline__ void load(Regs& r, int q, rsrc_t rs) const {
+        // k step j rides in the wave-uniform offset; a dead lane's offset
+        // stays past num_records (the host bounds BK * ld well below 2^31).
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r.v[q][j] = buf_load4s(rs, off[q], j * kstep);
+    }
+    __device__ __forceinline__ void store(const Regs& r, int q, half_t* tile, int tid) const {
+        const int dr = (tid % CG) * 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float col[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) col[j] = r.v[q][j][c];
+            lds_write8<BK>(tile, dr + c, dk[q] / 8, pack8(col));
+        }
+    }
+};
+
 // Bytes a K-contiguous stager's resource must span for a ROWS x BK tile with
 // leading dimension ld (host-side check against kMaxTileSpanBytes).
 inline int64_t span_kc(int rows, int bk, int64_t ld) { return ((int64_t)rows * ld + bk) * 4; }

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 
 #include "igemm.h"
 #include "runtime.h"
@@ -74,11 +75,25 @@ static __global__ void splitk_reduce(const float* __restrict__ P, float* __restr
     C[(i / N) * ldc + i % N] = s;
 }
 
+// Problems that declare `static constexpr bool kWsStream = true` supply
+// streaming stagers and run the large tile on igemm_ws2_kernel.
+template <class P, class = void>
+struct ws_stream : std::false_type {};
+template <class P>
+struct ws_stream<P, std::void_t<decltype(P::kWsStream)>> : std::bool_constant<P::kWsStream> {};
+
 template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
     if constexpr (BIG) {
         switch (t) {
-            case Tile::L: return launch_igemm_ws<256, 256, 32, 4, 2, 4>(p, splits, st);
+            case Tile::L:
+                if constexpr (ws_stream<P>::value) {
+                    // Split sizes are multiples of kBK, so K % 32 == 0 makes
+                    // every slice of every split whole.
+                    static_assert(kBK % 32 == 0, "split-K granularity must be whole slices");
+                    if (p.K % 32 == 0) return launch_igemm_ws2<256, 256, 32, 4, 2, 4>(p, splits, st);
+                }
+                return launch_igemm_ws<256, 256, 32, 4, 2, 4>(p, splits, st);
             case Tile::W: return launch_igemm<64, 256, 32, 1, 4>(p, splits, st);
             case Tile::M: return launch_igemm<128, 128, 32, 2, 2>(p, splits, st);
             default: break;

@@ -130,6 +130,24 @@ def test_square_sweep_config2(n):
         assert abs(float(np.sum(x.astype(np.float64) * g)) - ref) <= 1e-4 * abs(ref) + 1e-2
 
 
+@pytest.mark.parametrize("M,K,N,nb", [(4000, 4096, 3900, 1), (2000, 4128, 4000, 2),
+                                      (4096, 4100, 4096, 1)])
+def test_large_tile_edges(M, K, N, nb):
+    """256x256 tiles with partial edge tiles (M, N not multiples of 256); K a
+    multiple of 32 (streaming producers) and not (register-staged producers);
+    dB contracts over Nbatch*M."""
+    r = np.random.default_rng(M + 3 * K + 7 * N)
+    a = fp16r(r.uniform(-1, 1, (nb, M, K)))
+    b = fp16r(r.uniform(-1, 1, (K, N)))
+    dc = fp16r(r.uniform(-1, 1, (nb, M, N)))
+    got = hip_matmul(a, b)
+    assert_parity(got, S.matmul_batched(a, b), f"C {M}x{K}x{N}x{nb}")
+    da, db = hip_matmul_bwd(a, b, dc)
+    rda, rdb = S.matmul_bwd(a, b, dc)
+    assert_parity(da, rda, "dA")
+    assert_parity(db, rdb, "dB")
+
+
 def test_square_8192_sampled_rows():
     """n = 8192: 64 sampled rows of C, dA and columns of dB against fp64."""
     n = 8192
