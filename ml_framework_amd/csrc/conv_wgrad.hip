@@ -80,6 +80,38 @@ __device__ __forceinline__ half8 pick8(floatx4 w0, floatx4 w1, floatx4 w2) {
     return pack8(o);
 }
 
+// The 8 floats that start DD floats into the aligned 12-float window whose
+// quads sit at byte offsets o0, o1, o2 (kBufOOB: outside the image, reads 0).
+// Only those 8 floats are loaded: a loaded register that is never read would
+// be free for the register allocator to reuse while its load is in flight,
+// and the compiler then waits for that load to land (a full memory round trip
+// per step).
+template <int DD>
+__device__ __forceinline__ void load_x8(rsrc_t r, uint32_t o0, uint32_t o1, uint32_t o2,
+                                        float (&v)[8]) {
+    static_assert(DD == 0 || DD == 3, "exact X loads exist for misalignment 0 and 3");
+    const floatx4 mid = buf_load4(r, o1);
+    if constexpr (DD == 0) {
+        const floatx4 lo = buf_load4(r, o0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = lo[i];
+            v[4 + i] = mid[i];
+        }
+        (void)o2;
+    } else {
+        typedef float f3 __attribute__((ext_vector_type(3)));
+        const float lo = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o0 + 12u, 0, 0));
+        const f3 hi = __builtin_bit_cast(f3, __builtin_amdgcn_raw_buffer_load_b96(r, o2, 0, 0));
+        v[0] = lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[1 + i] = mid[i];
+        v[5] = hi[0];
+        v[6] = hi[1];
+        v[7] = hi[2];
+    }
+}
+
 // DD: the column misalignment (-pw) mod 4 when known at compile time (-1: any).
 template <int RR, int SS, int DD>
 __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) {
@@ -189,8 +221,10 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
 
     // ---- producers ----
     // X item (row of the group, channel, octet j): ring columns 8j..8j+7 hold
-    // X[.., ih, 8j - pw .. 8j - pw + 7]; loaded as three aligned float4s from
-    // column 8j - pw - dd and picked at offset dd (dd uniform). dY item (row,
+    // X[.., ih, 8j - pw .. 8j - pw + 7], which lie dd floats into the aligned
+    // 12-float window at column 8j - pw - dd. With dd known at compile time
+    // exactly those 8 floats are loaded (load_x8); otherwise the window's three
+    // float4s are loaded and picked at offset dd (dd uniform). dY item (row,
     // filter, octet j): columns 8j..8j+7 of the dY row (zero past Wo).
     // Buffer resources over this image's tile planes: out-of-range rows,
     // columns, channels and filters read 0.
@@ -230,7 +264,8 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         doff[k] = ((dfl[k] * a.Ho + ohA + drow[k]) * a.Wo + dcol[k]) * 4;
         dqm[k] = (dcol[k] < a.Wo ? 1 : 0) | (dcol[k] + 4 < a.Wo ? 2 : 0);
     }
-    floatx4 xv[kXI][3], dv[kDI][2];
+    floatx4 xv[kXI][3], dv[kDI][2];  // DD < 0: three aligned quads per X item
+    float xw[kXI][8];                // DD >= 0: exactly the item's 8 floats
 
     // Loads of X group rows [I0, I0 + NX) and dY output rows [O0, O0 + ND).
 #define SEERA_WG_LOAD(I0, NX, O0, ND)                                                      \
@@ -240,10 +275,14 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
             const int i = (I0) + xrow[k], ih = ih0 + i;                                    \
             const bool rok = xrow[k] < (NX) && (unsigned)i < (unsigned)need &&             \
                              (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C;            \
-            _Pragma("unroll") for (int q = 0; q < 3; ++q) {                                \
-                const uint32_t off = rok && ((xqm[k] >> q) & 1)                            \
-                    ? (uint32_t)(xoff[k] + xrb + 16 * q) : kBufOOB;                        \
-                xv[k][q] = buf_load4(xsrc, off);                                           \
+            uint32_t xo[3];                                                                \
+            _Pragma("unroll") for (int q = 0; q < 3; ++q)                                  \
+                xo[q] = rok && ((xqm[k] >> q) & 1) ? (uint32_t)(xoff[k] + xrb + 16 * q)    \
+                                                   : kBufOOB;                              \
+            if constexpr (DD >= 0) {                                                       \
+                load_x8<DD < 0 ? 0 : DD>(xsrc, xo[0], xo[1], xo[2], xw[k]);                \
+            } else {                                                                       \
+                _Pragma("unroll") for (int q = 0; q < 3; ++q) xv[k][q] = buf_load4(xsrc, xo[q]); \
             }                                                                              \
         }                                                                                  \
         const int drb = (O0) * a.Wo * 4;                                                   \
@@ -268,7 +307,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
             if (xrow[k] < (NX) && (unsigned)i < (unsigned)need) {                          \
                 half8 h;                                                                   \
                 if constexpr (DD >= 0) {                                                   \
-                    h = pick8<DD < 0 ? 0 : DD>(xv[k][0], xv[k][1], xv[k][2]);              \
+                    h = pack8(xw[k]);                                                      \
                 } else {                                                                   \
                     switch (dd) {                                                          \
                         case 0: h = pick8<0>(xv[k][0], xv[k][1], xv[k][2]); break;         \
