@@ -193,17 +193,19 @@ __global__ __launch_bounds__(kNT) void band_conv_kernel(const BandConvArgs a) {
 }
 
 // Wk[ftile][chunk][tap][f64][c32] for a forward convolution: W is [F, C, R, S].
+// Index math is 32-bit (the host keeps the prepared tensor below 2^31
+// elements): 64-bit division is a long software sequence on the GPU.
 __global__ void prep_fwd_weights(const float* __restrict__ W, half_t* __restrict__ wk, int F, int C,
-                                 int R, int S, int nchunks, int64_t total) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+                                 int R, int S, int nchunks, int total) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const int c32 = (int)(i & 31), f64 = (int)((i >> 5) & 63);
-    int64_t rest = i >> 11;
+    const int c32 = i & 31, f64 = (i >> 5) & 63;
+    int rest = i >> 11;
     const int taps = R * S;
-    const int tap = (int)(rest % taps);
+    const int tap = rest % taps;
     rest /= taps;
-    const int chunk = (int)(rest % nchunks);
-    const int ftile = (int)(rest / nchunks);
+    const int chunk = rest % nchunks;
+    const int ftile = rest / nchunks;
     const int f = ftile * 64 + f64, c = chunk * 32 + c32;
     const int t = tap / S, u = tap - t * S;
     float v = 0.f;
@@ -227,19 +229,19 @@ struct DgradPrepPhases {
 __global__ void prep_dgrad_weights(const float* __restrict__ W, half_t* __restrict__ wk, int Fc,
                                    int Cc, int R, int S, int sh, int sw, int nchunks,
                                    const DgradPrepPhases pp) {
-    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int gi = blockIdx.x * blockDim.x + threadIdx.x;  // < 2^31 (host check)
     if (gi >= pp.begin[pp.nphase]) return;
     int z = 0;
     while (z + 1 < pp.nphase && gi >= pp.begin[z + 1]) ++z;
-    const int64_t i = gi - pp.begin[z];
+    const int i = gi - (int)pp.begin[z];
     const int T = pp.T[z], U = pp.U[z];
-    const int k32 = (int)(i & 31), o64 = (int)((i >> 5) & 63);
-    int64_t rest = i >> 11;
+    const int k32 = i & 31, o64 = (i >> 5) & 63;
+    int rest = i >> 11;
     const int taps = T * U;
-    const int tap = (int)(rest % taps);
+    const int tap = rest % taps;
     rest /= taps;
-    const int chunk = (int)(rest % nchunks);
-    const int otile = (int)(rest / nchunks);
+    const int chunk = rest % nchunks;
+    const int otile = rest / nchunks;
     const int c = otile * 64 + o64;   // conv input channel = band output channel
     const int f = chunk * 32 + k32;   // conv output channel = band input channel
     const int t = tap / U, u = tap - t * U;
@@ -287,6 +289,159 @@ bool plan_tile(BandConvArgs& a) {
     return true;
 }
 
+// Software-pipelined variant of band_conv_kernel for small bands (the stride
+// phases of a transposed convolution): the loads of chunk ch+1 (weights and
+// band, into registers) are issued before the taps of chunk ch and written to
+// the other of two LDS stages after them, so the load latency hides behind
+// the MFMAs; one barrier per chunk. Same arithmetic, in the same order, as
+// band_conv_kernel. TAPS >= taps of every phase and ITEMS >= band items per
+// thread (host checks); the band is read through a buffer resource over one
+// image (host check: the image spans less than kMaxTileSpanBytes), so rows,
+// columns and channels outside it read 0.
+template <int PGW, int TAPS, int ITEMS>
+__global__ __launch_bounds__(kNT) void band_conv_pipe(const BandConvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    const int bx = blockIdx.x;
+    int z = 0;
+    while (z + 1 < a.nphase && bx >= a.ph[z + 1].block0) ++z;
+    const BandPhase& P = a.ph[z];
+    int local = bx - P.block0;
+    const int cb = local % P.ncb;
+    local /= P.ncb;
+    const int rb = local % P.nrb;
+    const int b = local / P.nrb;
+    const int oh0 = rb * a.TH, ow0 = cb * a.WC;
+    const int ftile = blockIdx.y;
+    const int taps = P.T * P.U;
+    const int stage = a.max_taps * 2048 + a.BR * a.BC4 * 32;  // halves per LDS stage
+
+    const int ir0 = oh0 * a.ish - P.iph;
+    const int icr = ow0 * a.isw - P.ipw;
+    const int ic0 = icr >= 0 ? (icr & ~3) : -((-icr + 3) & ~3);
+    const int coff = icr - ic0;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wf = wave & 1, wp = wave >> 1;
+    const int tile_px = a.TH * a.WC;
+    int pbase[PGW];
+#pragma unroll
+    for (int i = 0; i < PGW; ++i) {
+        int px = (wp * PGW + i) * 16 + (lane & 15);
+        if (px >= tile_px) px = 0;
+        const int ohl = px / a.WC, owl = px - ohl * a.WC;
+        pbase[i] = ohl * a.ish * a.BC4 + owl * a.isw + coff;
+    }
+    floatx4_t acc[2][PGW];
+#pragma unroll
+    for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+        for (int i = 0; i < PGW; ++i) acc[fi][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nq = a.BC4 >> 2;
+    const int band_items = a.BR * nq * 4;
+    const half_t* wsrc_base = a.wk + P.woff + (int64_t)ftile * a.nchunks * taps * 2048;
+    const rsrc_t isrc = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+    const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
+    // Per item: (row, quad, 8-channel group); the byte offset of its first
+    // element at channel 0 (kBufOOB: outside the image) and its band pixel.
+    uint32_t ioff[ITEMS];
+    int icg[ITEMS], ip0[ITEMS];
+    bool ilive[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const int it = tid + k * kNT;
+        ilive[k] = it < band_items;
+        const int cg = it & 3, rq = it >> 2;
+        const int r = rq / nq, q4 = rq - r * nq;
+        const int hin = ir0 + r, win = ic0 + q4 * 4;
+        const bool ok = ilive[k] && (unsigned)hin < (unsigned)a.H && (unsigned)win < (unsigned)a.W;
+        ioff[k] = ok ? (uint32_t)(((cg * 8) * a.H + hin) * a.W + win) * 4u : kBufOOB;
+        icg[k] = cg;
+        ip0[k] = r * a.BC4 + q4 * 4;
+    }
+    half8 wv[TAPS];
+    floatx4 bv[ITEMS][8];
+    auto load_chunk = [&](int ch) {
+        const half_t* wsrc = wsrc_base + (int64_t)ch * taps * 2048;
+#pragma unroll
+        for (int tp = 0; tp < TAPS; ++tp)
+            if (tp < taps) wv[tp] = *reinterpret_cast<const half8*>(wsrc + (tp * 256 + tid) * 8);
+        const uint32_t cbase = (uint32_t)(ch * 32) * cstride;
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // channel ch*32 + 8*cg + j: out of range channels read 0
+                const bool cok = ch * 32 + icg[k] * 8 + j < a.C;
+                bv[k][j] = buf_load4s(isrc, cok ? ioff[k] : kBufOOB, cbase + j * cstride);
+            }
+    };
+    auto store_chunk = [&](int stg) {
+        half_t* const wl = smem + stg * stage;
+        half_t* const bl = wl + a.max_taps * 2048;
+#pragma unroll
+        for (int tp = 0; tp < TAPS; ++tp)
+            if (tp < taps) lds_write8<32>(wl + tp * 2048, tid >> 2, tid & 3, wv[tp]);
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            if (!ilive[k]) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float col[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) col[j] = bv[k][j][q];
+                *reinterpret_cast<half8*>(bl + band_off(ip0[k] + q, icg[k])) = pack8(col);
+            }
+        }
+    };
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int ch = 0; ch < a.nchunks; ++ch) {
+        const bool more = ch + 1 < a.nchunks;
+        if (more) load_chunk(ch + 1);  // registers of chunk ch were written to LDS
+        const half_t* const wl = smem + (ch & 1) * stage;
+        const half_t* const bl = wl + a.max_taps * 2048;
+        for (int t = 0; t < P.T; ++t) {
+            for (int u = 0; u < P.U; ++u) {
+                const int tap = t * P.U + u;
+                const int tapoff = t * a.BC4 + u;
+                half8 fa[2], fb[PGW];
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+                    fa[fi] = lds_read8<32>(wl + tap * 2048, (wf * 2 + fi) * 16 + (lane & 15), lane >> 4);
+#pragma unroll
+                for (int i = 0; i < PGW; ++i)
+                    fb[i] = *reinterpret_cast<const half8*>(bl + band_off(pbase[i] + tapoff, lane >> 4));
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                    for (int i = 0; i < PGW; ++i) acc[fi][i] = mfma16x16x32(fa[fi], fb[i], acc[fi][i]);
+            }
+        }
+        if (more) store_chunk((ch + 1) & 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < PGW; ++i) {
+        const int px = (wp * PGW + i) * 16 + (lane & 15);
+        if (px >= tile_px) continue;
+        const int ohl = px / a.WC, owl = px - ohl * a.WC;
+        const int oh = oh0 + ohl, ow = ow0 + owl;
+        if (oh >= P.Ho || ow >= P.Wo) continue;
+        const int64_t opix = (int64_t)(oh * a.osh + P.oph) * a.Wout + ow * a.osw + P.opw;
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi) {
+            const int fb0 = ftile * 64 + (wf * 2 + fi) * 16 + 4 * (lane >> 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int f = fb0 + r;
+                if (f < a.F) a.out[((int64_t)b * a.F + f) * a.Hout * a.Wout + opix] = acc[fi][i][r];
+            }
+        }
+    }
+}
+
 template <int PGW>
 hipError_t launch_pgw(const BandConvArgs& a, hipStream_t st) {
     auto kern = band_conv_kernel<PGW>;
@@ -300,10 +455,40 @@ hipError_t launch_pgw(const BandConvArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+constexpr int kPipeTaps = 4, kPipeItems = 2;
+
+template <int PGW>
+hipError_t launch_pipe(const BandConvArgs& a, hipStream_t st) {
+    auto kern = band_conv_pipe<PGW, kPipeTaps, kPipeItems>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)a.lds_bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(a.nblocks, a.nftiles), dim3(kNT), (size_t)a.lds_bytes, st, a);
+    return hipGetLastError();
+}
+
 int launch_band(const BandConvArgs& a, hipStream_t st) {
     if (a.nblocks == 0 || a.nftiles == 0) return SEERA_OK;
     const int pgw = ceil_div(ceil_div(a.TH * a.WC, 16), 2);
     hipError_t e;
+    const int items = ceil_div(a.BR * (a.BC4 >> 2) * 4, kNT);
+    if (a.max_taps <= kPipeTaps && items <= kPipeItems && 2 * a.lds_bytes <= kBandMaxLds &&
+        (int64_t)a.C * a.H * a.W * 4 < kMaxTileSpanBytes) {
+        BandConvArgs p = a;
+        p.lds_bytes = 2 * a.lds_bytes;  // two stages
+        switch (pgw) {
+            case 1: e = launch_pipe<1>(p, st); break;
+            case 2: e = launch_pipe<2>(p, st); break;
+            case 3: e = launch_pipe<3>(p, st); break;
+            case 4: e = launch_pipe<4>(p, st); break;
+            case 5: e = launch_pipe<5>(p, st); break;
+            case 6: e = launch_pipe<6>(p, st); break;
+            default: e = launch_pipe<7>(p, st); break;
+        }
+        if (e != hipSuccess) return fail_hip(e, "band conv launch");
+        return SEERA_OK;
+    }
     switch (pgw) {
         case 1: e = launch_pgw<1>(a, st); break;
         case 2: e = launch_pgw<2>(a, st); break;
@@ -690,6 +875,73 @@ __global__ __launch_bounds__(kRedCols * kRedGroups) void wgrad_reduce(
     if (f < F && c < C) dW[((int64_t)f * C + c) * R * S + n / CT] = sum;
 }
 
+// Same sum with four consecutive partial columns per lane (16-byte loads;
+// needs CT*R*S % 4 == 0, so a lane's columns share one (tile, filter) row)
+// and eight groups of splits (measured: 7.3-7.8 us for cfg4's 37.7 MB; sixteen
+// groups with 16 loads in flight per thread were slower, 8.4-9.0 us). The
+// group sums are added in group order, as above.
+constexpr int kRed4Lanes = 64, kRed4Groups = 8, kRed4Unroll = 8;
+__global__ __launch_bounds__(kRed4Lanes * kRed4Groups) void wgrad_reduce4(
+    const float* __restrict__ part, float* __restrict__ dW, int F, int C, int R, int S, int CT,
+    int nctile, int ntiles, int nsplit) {
+    __shared__ floatx4 red[kRed4Groups][kRed4Lanes];
+    const int ntot = CT * R * S;
+    const int lane = threadIdx.x % kRed4Lanes, grp = threadIdx.x / kRed4Lanes;
+    const int64_t i = ((int64_t)blockIdx.x * kRed4Lanes + lane) * 4;  // first of 4 columns
+    const bool live = i < (int64_t)ntiles * 64 * ntot;
+    const int n = live ? (int)(i % ntot) : 0;
+    const int f64 = live ? (int)((i / ntot) % 64) : 0;
+    const int ty = live ? (int)(i / ((int64_t)64 * ntot)) : 0;
+    const float* p = part + ((int64_t)ty * nsplit * 64 + f64) * ntot + n;
+    const int64_t zstride = (int64_t)64 * ntot;
+    const int per = (nsplit + kRed4Groups - 1) / kRed4Groups;
+    const int z0 = grp * per, z1 = min(nsplit, z0 + per);
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        int z = z0;
+        for (; z + kRed4Unroll <= z1; z += kRed4Unroll) {
+            floatx4 v[kRed4Unroll];
+#pragma unroll
+            for (int u = 0; u < kRed4Unroll; ++u)
+                v[u] = *reinterpret_cast<const floatx4*>(p + (z + u) * zstride);
+#pragma unroll
+            for (int u = 0; u < kRed4Unroll; ++u) acc += v[u];
+        }
+        for (; z < z1; ++z) acc += *reinterpret_cast<const floatx4*>(p + z * zstride);
+    }
+    red[grp][lane] = acc;
+    __syncthreads();
+    if (grp != 0 || !live) return;
+    floatx4 sum = red[0][lane];
+#pragma unroll
+    for (int g = 1; g < kRed4Groups; ++g) sum += red[g][lane];
+    const int f = (ty / nctile) * 64 + f64;
+    if (f >= F) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int nq = n + q;
+        const int c = (ty % nctile) * CT + nq % CT;
+        if (c < C) dW[((int64_t)f * C + c) * R * S + nq / CT] = sum[q];
+    }
+}
+
+// Adds the partials of `ntiles` (tile, filter) rows of CT*R*S columns.
+hipError_t launch_wgrad_reduce(const float* part, float* dW, int F, int C, int R, int S, int CT,
+                               int nctile, int ntiles, int nsplit, hipStream_t st) {
+    const int64_t total = (int64_t)ntiles * 64 * CT * R * S;
+    if ((CT * R * S) % 4 == 0) {
+        const int64_t cols = kRed4Lanes * 4;
+        hipLaunchKernelGGL(wgrad_reduce4, dim3((unsigned)((total + cols - 1) / cols)),
+                           dim3(kRed4Lanes * kRed4Groups), 0, st, part, dW, F, C, R, S, CT,
+                           nctile, ntiles, nsplit);
+    } else {
+        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
+                           dim3(kRedCols * kRedGroups), 0, st, part, dW, F, C, R, S, CT, nctile,
+                           ntiles, nsplit);
+    }
+    return hipGetLastError();
+}
+
 template <int SW, int NCH>
 hipError_t launch_wgrad_sw(const WgradArgs& a, int ngw, hipStream_t st) {
     const void* k = nullptr;
@@ -748,11 +1000,12 @@ int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H
     a.nftiles = ceil_div(F, 64);
     if (!plan_tile(a)) return SEERA_OK;
     const int64_t wsz = (int64_t)a.nftiles * a.nchunks * R * S * 2048;
+    if (wsz > 0x7fffffff) return SEERA_OK;  // prep kernel indexes in 32 bits
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(half_t) * (size_t)wsz, &ws));
     a.wk = static_cast<const half_t*>(ws);
     hipLaunchKernelGGL(prep_fwd_weights, dim3((unsigned)((wsz + 255) / 256)), dim3(256), 0, st, Wt,
-                       static_cast<half_t*>(ws), F, C, R, S, a.nchunks, wsz);
+                       static_cast<half_t*>(ws), F, C, R, S, a.nchunks, (int)wsz);
     SEERA_HIP_TRY(hipGetLastError());
     bool streamed = false;
     SEERA_TRY(stream_conv(a, st, &streamed));
@@ -802,6 +1055,7 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
         }
     a.nphase = zi;
     if (!plan_tile(a)) return SEERA_OK;
+    if (woff > 0x7fffffff) return SEERA_OK;  // prep kernel indexes in 32 bits
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(half_t) * (size_t)std::max<int64_t>(woff, 1), &ws));
     a.wk = static_cast<const half_t*>(ws);
@@ -838,11 +1092,8 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
         bool streamed = false;
         SEERA_TRY(stream_wgrad_partials(Y, X, B, C, H, W, F, R, S, ph, pw, st, &wp, &streamed));
         if (streamed) {
-            const int64_t total = (int64_t)wp.ntiles * 64 * wp.CT * R * S;
-            hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
-                               dim3(kRedCols * kRedGroups), 0, st, wp.part, dW, F, C, R, S, wp.CT,
-                               wp.nctile, wp.ntiles, wp.nsplit);
-            SEERA_HIP_TRY(hipGetLastError());
+            SEERA_HIP_TRY(launch_wgrad_reduce(wp.part, dW, F, C, R, S, wp.CT, wp.nctile, wp.ntiles,
+                                              wp.nsplit, st));
             *used = true;
             return SEERA_OK;
         }
@@ -910,11 +1161,7 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     if (sw == 1) e = nch == 2 ? launch_wgrad_sw<1, 2>(a, ngw, st) : launch_wgrad_sw<1, 1>(a, ngw, st);
     else e = nch == 2 ? launch_wgrad_sw<2, 2>(a, ngw, st) : launch_wgrad_sw<2, 1>(a, ngw, st);
     if (e != hipSuccess) return fail_hip(e, "band wgrad launch");
-    const int64_t total = (int64_t)tiles * 64 * ntot;
-    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
-                       dim3(kRedCols * kRedGroups), 0, st, a.part, dW, F, C, R, S, a.CT, a.nctile,
-                       tiles, a.nsplit);
-    SEERA_HIP_TRY(hipGetLastError());
+    SEERA_HIP_TRY(launch_wgrad_reduce(a.part, dW, F, C, R, S, a.CT, a.nctile, tiles, a.nsplit, st));
     *used = true;
     return SEERA_OK;
 }
