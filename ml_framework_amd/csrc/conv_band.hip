@@ -776,59 +776,69 @@ __global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
             }                                                                               \
         }                                                                                   \
     }
-    // Issue the global loads of step J into DYV/XW.
+    // Issue the global loads of step J into DYV/XW. Every lane issues the same
+    // loads in every step (out-of-range elements, lanes without an item and
+    // the X tail beyond XI::F4 get offsets past num_records and read 0): with
+    // a fixed load count the compiler's vmcnt waits stay exact, and a write
+    // waits only for its own step's loads, not for the step issued after it.
+    // Buffer resources cover this image's dY rows of the filter tile and its
+    // X planes (host check: each spans less than kMaxTileSpanBytes).
 #define SEERA_WG_LOAD(J, DYV, XW)                                                           \
     {                                                                                       \
         const int item = it0 + (J) / NCH, ch = (J) % NCH;                                   \
         const int b = tile_b(item), oh0 = tile_oh0(item), ow0 = tile_ow0(item);             \
         if (ch == 0) {                                                                      \
+            const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + ftile * 64) * a.Ho * a.Wo); \
             _Pragma("unroll") for (int kk = 0; kk < kWgDyMax; ++kk) {                       \
                 const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16; \
                 const int oh = oh0 + ohl, ow = ow0 + 8 * m;                                 \
                 const bool ok = dyit[kk] >= 0 && fl < f_lim && oh < a.Ho;                   \
-                const float* src =                                                          \
-                    a.dy + (((int64_t)b * a.F + ftile * 64 + fl) * a.Ho + oh) * a.Wo + ow;  \
-                _Pragma("unroll") for (int h = 0; h < 2; ++h) {                             \
-                    DYV[kk][h] = floatx4{0.f, 0.f, 0.f, 0.f};                               \
-                    if (ok && ow + 4 * h < a.Wo)                                            \
-                        DYV[kk][h] = *reinterpret_cast<const floatx4*>(src + 4 * h);        \
-                }                                                                           \
+                const uint32_t off = (uint32_t)(((fl * a.Ho + oh) * a.Wo + ow) * 4);        \
+                _Pragma("unroll") for (int h = 0; h < 2; ++h)                               \
+                    DYV[kk][h] = buf_load4(dsrc,                          \
+                                           ok && ow + 4 * h < a.Wo ? off + 16u * h : kBufOOB); \
             }                                                                               \
         }                                                                                   \
-        if (xit >= 0) {                                                                     \
+        {                                                                                   \
             const int cl = xit & 255, row = (xit >> 8) & 255, grp = xit >> 16;              \
             const int c = ctile * a.CT + ch * 32 + cl, hin = oh0 * a.sh - a.ph + row;       \
             const int a0 = floor4(ow0 * a.sw - a.pw) + 8 * XI::OCT * grp * SW;              \
-            const bool rowok = c < a.C && (unsigned)hin < (unsigned)a.H;                    \
-            const float* src = a.x + (((int64_t)b * a.C + c) * a.H + hin) * a.W;            \
+            const bool rowok = xit >= 0 && c < a.C && (unsigned)hin < (unsigned)a.H;        \
+            const rsrc_t xsrc = make_rsrc(a.x + (int64_t)b * a.C * a.H * a.W);              \
+            const int rbase = rowok ? (c * a.H + hin) * a.W : 0;                            \
             _Pragma("unroll") for (int q = 0; q < 11; ++q) {                                \
                 const int col = a0 + 4 * q;                                                 \
                 floatx4 x4 = {0.f, 0.f, 0.f, 0.f};                                          \
-                if (q < XI::F4 && rowok && (unsigned)col < (unsigned)a.W)                   \
-                    x4 = *reinterpret_cast<const floatx4*>(src + col);                      \
+                if (q < XI::F4)                                                             \
+                    x4 = buf_load4(xsrc, rowok && (unsigned)col < (unsigned)a.W             \
+                                             ? (uint32_t)((rbase + col) * 4) : kBufOOB);    \
                 _Pragma("unroll") for (int e = 0; e < 4; ++e) XW[4 * q + e] = x4[e];        \
             }                                                                               \
         }                                                                                   \
     }
 
     // Steps 0 and 1 in flight, then per step j: write j, load j+2 into the
-    // registers j just freed, and meet the consumers at the barrier that
-    // releases step j to them.
-    if (nsteps > 0) SEERA_WG_LOAD(0, dyv0, xw0)
-    if (nsteps > 1) SEERA_WG_LOAD(1, dyv1, xw1)
-    for (int j = 0; j < nsteps; j += 2) {
+    // registers j just freed (past the last step: the last step again, never
+    // written), and meet the consumers at the barrier that releases step j.
+    if (nsteps == 0) return;
+    SEERA_WG_LOAD(0, dyv0, xw0)
+    SEERA_WG_LOAD(min(1, nsteps - 1), dyv1, xw1)
+    int j = 0;
+    for (; j + 1 < nsteps; j += 2) {
         SEERA_WG_WRITE(j, dyv0, xw0)
-        if (j + 2 < nsteps) SEERA_WG_LOAD(j + 2, dyv0, xw0)
+        SEERA_WG_LOAD(min(j + 2, nsteps - 1), dyv0, xw0)
         __syncthreads();
-        if (j + 1 < nsteps) {
-            SEERA_WG_WRITE(j + 1, dyv1, xw1)
-            if (j + 3 < nsteps) SEERA_WG_LOAD(j + 3, dyv1, xw1)
-            __syncthreads();
-        }
+        SEERA_WG_WRITE(j + 1, dyv1, xw1)
+        SEERA_WG_LOAD(min(j + 3, nsteps - 1), dyv1, xw1)
+        __syncthreads();
+    }
+    if (j < nsteps) {
+        SEERA_WG_WRITE(j, dyv0, xw0)
+        __syncthreads();
     }
 #undef SEERA_WG_WRITE
 #undef SEERA_WG_LOAD
-    if (nsteps == 0) return;
+    __builtin_amdgcn_s_waitcnt(0);  // the unused last loads land before the wave ends
     __syncthreads();  // matches the consumers' final barrier
 }
 
@@ -1100,6 +1110,11 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     }
     if (Wo % 4 != 0 || W % 4 != 0 || sw > 2 || S > 7 || R * S > 18 || !aligned16(Y) ||
         !aligned16(X) || B == 0)
+        return SEERA_OK;
+    // The producers' buffer resources span one image's X planes and 65 dY
+    // planes (a 64-filter tile plus the row overrun of a partial tile).
+    if ((int64_t)(C + 64) * H * W * 4 >= kMaxTileSpanBytes ||
+        (int64_t)65 * Ho * Wo * 4 >= kMaxTileSpanBytes)
         return SEERA_OK;
     WgradArgs a{};
     a.dy = Y; a.x = X;
