@@ -41,8 +41,20 @@ int seera_hip_device_count(void);
 
 /* cuda_malloc / cuda_malloc_f32 / _i32 / _i16 / _f16 (cuda_bindings.cpp:23-56). */
 int seera_hip_malloc(void **out, size_t nbytes);
-/* cuda_free (cuda_bindings.cpp:58-59). NULL is a no-op. */
+/* cuda_free (cuda_bindings.cpp:58-59). NULL is a no-op. Blocks from
+ * seera_hip_malloc go back to a per-device cache of their size class and are
+ * handed out again; if an *_async entry point (or a memset / device copy) may
+ * still have work queued, the device is synchronized first, as cudaFree does. */
 int seera_hip_free(void *ptr);
+/* No counterpart in the reference: hands every cached block back to HIP
+ * (after a device synchronize), for callers that need the memory elsewhere. */
+int seera_hip_empty_cache(void);
+/* No counterpart in the reference: bytes held by live allocations and by the
+ * cache (size classes: 512 B, powers of two up to 1 MiB, multiples of 2 MiB). */
+int seera_hip_memory_stats(size_t *live_bytes, size_t *cached_bytes);
+/* cuda_ones_f / cuda_zeros_f (cuda_bindings.cpp:467-477) fill what they
+ * allocate: ptr[0, count) = value. Synchronous. */
+int seera_hip_fill_f32(float *ptr, float value, size_t count);
 /* cuda_memset (cuda_bindings.cpp:65-66). */
 int seera_hip_memset(void *ptr, int value, size_t nbytes);
 /* cuda_memcopy_devicetodevice (cuda_bindings.cpp:61-62): dst <- src. */

@@ -20,7 +20,14 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 
 def seera_cuda():
     """Import the compiled ``seera_cuda`` module (raises if not built)."""
-    return importlib.import_module("ml_framework_amd.seera_cuda")
+    mod = importlib.import_module("ml_framework_amd.seera_cuda")
+    # Importing the submodule binds it to this package's attribute of the same
+    # name; put the loader back so that later calls keep working.
+    globals()["seera_cuda"] = _load_seera_cuda
+    return mod
+
+
+_load_seera_cuda = seera_cuda
 
 
 def install_seera_cuda() -> None:

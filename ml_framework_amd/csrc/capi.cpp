@@ -23,7 +23,14 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 int sync_after(int status) {
     if (status != SEERA_OK) return status;
     SEERA_HIP_TRY(hipDeviceSynchronize());
+    note_device_synchronized();
     return SEERA_OK;
+}
+// *_async entry points: the enqueued work may still use its buffers after the
+// call returns, so the next free synchronizes first.
+int queued(int status) {
+    if (status == SEERA_OK) note_async_work();
+    return status;
 }
 
 bool nonneg(int a) { return a >= 0; }
@@ -160,15 +167,21 @@ int seera_hip_device_count(void) {
 int seera_hip_malloc(void** out, size_t nbytes) {
     return guarded([&] {
         if (!out) return fail(SEERA_ERR_INVALID_ARGUMENT, "null out pointer");
-        *out = nullptr;
-        SEERA_HIP_TRY(hipMalloc(out, nbytes == 0 ? 1 : nbytes));
-        return (int)SEERA_OK;
+        return device_malloc(out, nbytes);
     });
 }
 
 int seera_hip_free(void* ptr) {
+    return guarded([&] { return device_free(ptr); });
+}
+
+int seera_hip_empty_cache(void) {
+    return guarded([&] { return device_empty_cache(); });
+}
+
+int seera_hip_memory_stats(size_t* live_bytes, size_t* cached_bytes) {
     return guarded([&] {
-        if (ptr) SEERA_HIP_TRY(hipFree(ptr));
+        device_memory_stats(live_bytes, cached_bytes);
         return (int)SEERA_OK;
     });
 }
@@ -178,7 +191,15 @@ int seera_hip_memset(void* ptr, int value, size_t nbytes) {
         if (nbytes == 0) return (int)SEERA_OK;
         if (!ptr) return fail(SEERA_ERR_INVALID_ARGUMENT, "null device pointer");
         SEERA_HIP_TRY(hipMemset(ptr, value, nbytes));
-        return (int)SEERA_OK;
+        return queued(SEERA_OK);
+    });
+}
+
+int seera_hip_fill_f32(float* ptr, float value, size_t count) {
+    return guarded([&] {
+        if (count == 0) return (int)SEERA_OK;
+        if (!ptr) return fail(SEERA_ERR_INVALID_ARGUMENT, "null device pointer");
+        return sync_after(fill_f32(ptr, value, count, nullptr));
     });
 }
 
@@ -192,7 +213,8 @@ static int copy(void* dst, const void* src, size_t nbytes, hipMemcpyKind kind) {
 }
 
 int seera_hip_memcpy_d2d(void* dst, const void* src, size_t n) {
-    return copy(dst, src, n, hipMemcpyDeviceToDevice);
+    // A device-to-device hipMemcpy may return before the copy has run.
+    return queued(copy(dst, src, n, hipMemcpyDeviceToDevice));
 }
 int seera_hip_memcpy_h2d(void* dst, const void* src, size_t n) {
     return copy(dst, src, n, hipMemcpyHostToDevice);
@@ -204,13 +226,14 @@ int seera_hip_memcpy_d2h(void* dst, const void* src, size_t n) {
 int seera_hip_synchronize(void) {
     return guarded([&] {
         SEERA_HIP_TRY(hipDeviceSynchronize());
+        note_device_synchronized();
         return (int)SEERA_OK;
     });
 }
 
 int seera_hip_matmul_async(const float* A, const float* B, float* C, int M, int N, int K,
                            int Nbatch, void* stream) {
-    return guarded([&] { return matmul_impl(A, B, C, M, N, K, Nbatch, as_stream(stream)); });
+    return guarded([&] { return queued(matmul_impl(A, B, C, M, N, K, Nbatch, as_stream(stream))); });
 }
 int seera_hip_matmul(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch) {
     return guarded([&] { return sync_after(matmul_impl(A, B, C, M, N, K, Nbatch, nullptr)); });
@@ -219,7 +242,7 @@ int seera_hip_matmul(const float* A, const float* B, float* C, int M, int N, int
 int seera_hip_matmul_bwd_async(const float* A, const float* B, const float* dC, float* dA,
                                float* dB, int M, int N, int K, int Nbatch, void* stream) {
     return guarded(
-        [&] { return matmul_bwd_impl(A, B, dC, dA, dB, M, N, K, Nbatch, as_stream(stream)); });
+        [&] { return queued(matmul_bwd_impl(A, B, dC, dA, dB, M, N, K, Nbatch, as_stream(stream))); });
 }
 int seera_hip_matmul_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB,
                          int M, int N, int K, int Nbatch) {
@@ -248,8 +271,8 @@ int seera_hip_conv2d_fwd_async(const float* image, const float* kernel, float* c
                                int C, int H, int W, int N, int R, int S, int pad_h, int pad_w,
                                int stride_h, int stride_w, void* stream) {
     return guarded([&] {
-        return conv2d_fwd_impl(image, kernel, conv, batchN, C, H, W, N, R, S, pad_h, pad_w,
-                               stride_h, stride_w, as_stream(stream));
+        return queued(conv2d_fwd_impl(image, kernel, conv, batchN, C, H, W, N, R, S, pad_h,
+                                      pad_w, stride_h, stride_w, as_stream(stream)));
     });
 }
 int seera_hip_conv2d_fwd(const float* image, const float* kernel, float* conv, int batchN, int C,
@@ -265,8 +288,8 @@ int seera_hip_conv2d_bwd_async(const float* W, const float* X, const float* dY, 
                                float* dW, int batch, int C, int H, int W_in, int N, int R, int S,
                                int strideh, int stridew, int padh, int padw, void* stream) {
     return guarded([&] {
-        return conv2d_bwd_impl(W, X, dY, dX, dW, batch, C, H, W_in, N, R, S, strideh, stridew,
-                               padh, padw, as_stream(stream));
+        return queued(conv2d_bwd_impl(W, X, dY, dX, dW, batch, C, H, W_in, N, R, S, strideh,
+                                      stridew, padh, padw, as_stream(stream)));
     });
 }
 int seera_hip_conv2d_bwd(const float* W, const float* X, const float* dY, float* dX, float* dW,
@@ -283,8 +306,8 @@ int seera_hip_conv2DTranpose_fwd_async(const float* X, const float* W, float* ou
                                        int strideh, int stridew, int padh, int padw,
                                        void* stream) {
     return guarded([&] {
-        return convT_fwd_impl(X, W, out, batch, Cin, Hin, Win, Cout, KH, KW, strideh, stridew,
-                              padh, padw, as_stream(stream));
+        return queued(convT_fwd_impl(X, W, out, batch, Cin, Hin, Win, Cout, KH, KW, strideh,
+                                     stridew, padh, padw, as_stream(stream)));
     });
 }
 int seera_hip_conv2DTranpose_fwd(const float* X, const float* W, float* out, int batch, int Cin,
@@ -301,8 +324,8 @@ int seera_hip_conv2DTranspose_bwd_async(const float* W, const float* X, const fl
                                         int Win, int Cout, int KH, int KW, int strideh,
                                         int stridew, int padh, int padw, void* stream) {
     return guarded([&] {
-        return convT_bwd_impl(W, X, dY, dX, dW, batch, Cin, Hin, Win, Cout, KH, KW, strideh,
-                              stridew, padh, padw, as_stream(stream));
+        return queued(convT_bwd_impl(W, X, dY, dX, dW, batch, Cin, Hin, Win, Cout, KH, KW,
+                                     strideh, stridew, padh, padw, as_stream(stream)));
     });
 }
 int seera_hip_conv2DTranspose_bwd(const float* W, const float* X, const float* dY, float* dX,

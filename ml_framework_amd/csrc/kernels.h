@@ -15,6 +15,9 @@ int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* 
 // out[b, c, r] = in[b, r, c] for b < batch.
 int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st);
 
+// p[0, n) = v.
+int fill_f32(float* p, float v, size_t n, hipStream_t st);
+
 // Y[B, F, Ho, Wo] = conv(X[B, C, H, W], Wt[F, C, R, S]).
 int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
              int S, int sh, int sw, int ph, int pw, hipStream_t st);

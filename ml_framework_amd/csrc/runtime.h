@@ -33,6 +33,18 @@ void clear_error();
 // concurrent calls from several host threads on one device.
 int workspace(size_t bytes, void** out);
 
+// Caching device allocator behind seera_hip_malloc / seera_hip_free (size
+// classes per device; see runtime.cpp). A free synchronizes the device first
+// when an *_async entry point may have left work queued.
+int device_malloc(void** out, size_t nbytes);
+int device_free(void* ptr);
+int device_empty_cache();
+void device_memory_stats(size_t* live_bytes, size_t* cached_bytes);
+// Called by the *_async entry points after they enqueue work, and after every
+// device-wide synchronization.
+void note_async_work();
+void note_device_synchronized();
+
 // Launch-shape sanity: every grid the library builds must fit these limits.
 constexpr int64_t kMaxGridX = 0x7fffffff;
 

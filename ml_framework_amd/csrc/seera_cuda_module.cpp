@@ -10,6 +10,7 @@
 #include <pybind11/stl.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -99,6 +100,31 @@ PYBIND11_MODULE(seera_cuda, m) {
               check(seera_hip_memset(dev<void>(p), value, n_bytes));
           },
           "Memset GPU memory");
+    // cuda_bindings.cpp:467-477: allocate total_elements floats and fill them.
+    m.def("cuda_ones_f",
+          [](int total_elements) {
+              const uintptr_t p = alloc_bytes((size_t)std::max(total_elements, 0) * sizeof(float));
+              check(seera_hip_fill_f32(dev<float>(p), 1.f, (size_t)std::max(total_elements, 0)));
+              return p;
+          },
+          "Allocate total_elements floats filled with 1 (GPU ptr)");
+    m.def("cuda_zeros_f",
+          [](int total_elements) {
+              const uintptr_t p = alloc_bytes((size_t)std::max(total_elements, 0) * sizeof(float));
+              check(seera_hip_fill_f32(dev<float>(p), 0.f, (size_t)std::max(total_elements, 0)));
+              return p;
+          },
+          "Allocate total_elements floats filled with 0 (GPU ptr)");
+    // Not in the reference: the caching allocator behind cuda_malloc / cuda_free.
+    m.def("cuda_empty_cache", []() { check(seera_hip_empty_cache()); },
+          "Return the allocator's cached blocks to HIP");
+    m.def("cuda_memory_stats",
+          []() {
+              size_t live = 0, cached = 0;
+              check(seera_hip_memory_stats(&live, &cached));
+              return py::make_tuple(live, cached);
+          },
+          "(bytes in live allocations, bytes cached for reuse)");
 
     // ---- transfers (cuda_bindings.cpp:73-170) ----
     m.def("to_device_f16", [](arr_f a) { return upload<float>(a); },

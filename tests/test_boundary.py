@@ -78,6 +78,8 @@ REFERENCE_SIGNATURES = {
     "cuda_conv2d_bwd": 16,               # 302 (..., strideh, stridew, padh, padw)
     "cuda_conv2DTranpose_fwd": 14,       # 316 [sic]
     "cuda_conv2DTranspose_bwd": 16,      # 324
+    "cuda_ones_f": 1,                    # 467 (total_elements) -> device pointer
+    "cuda_zeros_f": 1,                   # 474 (total_elements) -> device pointer
 }
 
 
