@@ -175,10 +175,38 @@ def bench_mlp(steps, warmup, stream):
 
     grads[3].fill(0)
     ms = timed(step, steps, warmup, stream)
-    for v in acts + ws + grads + dws:
+    # The Dense forward the reference runs as matmul + broadcast_add_4d + relu
+    # per layer, with bias and ReLU (and its mask) fused into the GEMM store,
+    # next to the same three GEMMs alone; and the three bias gradients.
+    biases = [DeviceBuffer.from_array(r.uniform(-0.1, 0.1, o).astype(np.float32)) for o in dims[1:]]
+    masks = [DeviceBuffer(256 * o * 4) for o in dims[1:]]
+    dbs = [DeviceBuffer(o * 4) for o in dims[1:]]
+
+    def fwd_plain():
+        for li in range(3):
+            capi.check(lib.seera_hip_matmul_async(acts[li].ptr, ws[li].ptr, acts[li + 1].ptr, 256,
+                                                  dims[li + 1], dims[li], 1, stream.ptr))
+
+    def fwd_fused():
+        for li in range(3):
+            act = capi.SEERA_ACT_RELU if li < 2 else capi.SEERA_ACT_NONE
+            capi.check(lib.seera_hip_matmul_bias_act_async(
+                acts[li].ptr, ws[li].ptr, biases[li].ptr, acts[li + 1].ptr, masks[li].ptr, 256,
+                dims[li + 1], dims[li], 1, act, stream.ptr))
+
+    def bias_grads():
+        for li in range(3):
+            capi.check(lib.seera_hip_bias_grad_async(grads[li + 1].ptr, dbs[li].ptr, 256,
+                                                     dims[li + 1], stream.ptr))
+
+    ms_plain = timed(fwd_plain, steps, warmup, stream)
+    ms_fused = timed(fwd_fused, steps, warmup, stream)
+    ms_db = timed(bias_grads, steps, warmup, stream)
+    for v in acts + ws + grads + dws + biases + masks + dbs:
         v.close()
     flops = sum(2 * 256 * i * o * 3 for i, o in zip(dims[:-1], dims[1:]))
-    return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "ms_fwd_gemms": ms_plain, "ms_fwd_fused_bias_relu": ms_fused, "ms_bias_grads": ms_db}
 
 
 def cpu_baseline(n=4096, reps=5):

@@ -85,6 +85,30 @@ int seera_hip_matmul_bwd_async(const float *A, const float *B, const float *dC,
                                float *dA, float *dB, int M, int N, int K,
                                int Nbatch, void *stream);
 
+/* No single counterpart in the reference: the Dense-layer forward it runs as
+ * three calls -- cuda_matmul (GEMM.cu:95-103), broadcast_add_4d of the bias
+ * (broadcast.cu:12-64, 140-146) and cuda_relu_fwd (activations.cu:9-15) --
+ * fused into the GEMM's store: C = act(A . B + bias[n]), with bias [N] (NULL:
+ * none) added in fp32 and act SEERA_ACT_NONE or SEERA_ACT_RELU. ReLU gives
+ * C = v > 0 ? v : 0 and, when mask is non-NULL, mask = v > 0 ? 1 : 0 (the
+ * reference's relu grad buffer), [Nbatch*M, N] like C. Bit-identical to the
+ * three calls. */
+enum { SEERA_ACT_NONE = 0, SEERA_ACT_RELU = 1 };
+int seera_hip_matmul_bias_act(const float *A, const float *B, const float *bias,
+                              float *C, float *mask, int M, int N, int K,
+                              int Nbatch, int act);
+int seera_hip_matmul_bias_act_async(const float *A, const float *B,
+                                    const float *bias, float *C, float *mask,
+                                    int M, int N, int K, int Nbatch, int act,
+                                    void *stream);
+
+/* The bias gradient the reference takes with Reductionsum over the batch
+ * (reductionKernels.cu:12-29 via Seera_Engine.py:43-65): db[n] = sum over
+ * rows of dY [rows, N], in a fixed order. */
+int seera_hip_bias_grad(const float *dY, float *db, int rows, int N);
+int seera_hip_bias_grad_async(const float *dY, float *db, int rows, int N,
+                              void *stream);
+
 /* cuda_transpose_2d (GEMM.cu:229-235; binding cuda_bindings.cpp:276-280).
  * out[c,r] = in[r,c], bit-exact. */
 int seera_hip_transpose_2d(const float *in, float *out, int rows, int cols);

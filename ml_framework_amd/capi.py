@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(PKG, "libseera_hip.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "seera_hip.h")
 
 SEERA_OK = 0
+SEERA_ACT_NONE, SEERA_ACT_RELU = 0, 1
 SEERA_ERR_INVALID_ARGUMENT = 1
 SEERA_ERR_HIP = 2
 SEERA_ERR_OUT_OF_MEMORY = 3
@@ -40,6 +41,10 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_synchronize": ([], _i),
     "seera_hip_matmul": ([_vp, _vp, _vp, _i, _i, _i, _i], _i),
     "seera_hip_matmul_async": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "seera_hip_matmul_bias_act": ([_vp] * 5 + [_i] * 5, _i),
+    "seera_hip_matmul_bias_act_async": ([_vp] * 5 + [_i] * 5 + [_vp], _i),
+    "seera_hip_bias_grad": ([_vp, _vp, _i, _i], _i),
+    "seera_hip_bias_grad_async": ([_vp, _vp, _i, _i, _vp], _i),
     "seera_hip_matmul_bwd": ([_vp] * 5 + [_i] * 4, _i),
     "seera_hip_matmul_bwd_async": ([_vp] * 5 + [_i] * 4 + [_vp], _i),
     "seera_hip_transpose_2d": ([_vp, _vp, _i, _i], _i),

@@ -64,6 +64,23 @@ int matmul_impl(const float* A, const float* B, float* C, int M, int N, int K, i
     return gemm_fwd(A, B, C, M, N, K, Nbatch, st);
 }
 
+int matmul_bias_act_impl(const float* A, const float* B, const float* bias, float* C, float* mask,
+                         int M, int N, int K, int Nbatch, int act, hipStream_t st) {
+    if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "matmul dims must be >= 0 (M=%d N=%d K=%d Nbatch=%d)",
+                    M, N, K, Nbatch);
+    if (act != SEERA_ACT_NONE && act != SEERA_ACT_RELU)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "unknown activation %d", act);
+    const bool work = prod(M, N, Nbatch) > 0;
+    SEERA_TRY(check_ptrs(work, C, work && K > 0 ? A : C, work && K > 0 ? B : C));
+    return gemm_fwd_bias_act(A, B, bias, C, act == SEERA_ACT_RELU ? mask : nullptr, M, N, K,
+                             Nbatch, act, st);
+}
+int bias_grad_impl(const float* dY, float* db, int rows, int N, hipStream_t st) {
+    if (rows < 0 || N < 0) return fail(SEERA_ERR_INVALID_ARGUMENT, "bias_grad dims must be >= 0");
+    SEERA_TRY(check_ptrs(N > 0, db, rows > 0 ? dY : db, db));
+    return bias_grad(dY, db, rows, N, st);
+}
 int matmul_bwd_impl(const float* A, const float* B, const float* dC, float* dA, float* dB, int M,
                     int N, int K, int Nbatch, hipStream_t st) {
     if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
@@ -249,6 +266,28 @@ int seera_hip_matmul_bwd(const float* A, const float* B, const float* dC, float*
     return guarded([&] {
         return sync_after(matmul_bwd_impl(A, B, dC, dA, dB, M, N, K, Nbatch, nullptr));
     });
+}
+
+int seera_hip_matmul_bias_act_async(const float* A, const float* B, const float* bias, float* C,
+                                    float* mask, int M, int N, int K, int Nbatch, int act,
+                                    void* stream) {
+    return guarded([&] {
+        return queued(matmul_bias_act_impl(A, B, bias, C, mask, M, N, K, Nbatch, act,
+                                           as_stream(stream)));
+    });
+}
+int seera_hip_matmul_bias_act(const float* A, const float* B, const float* bias, float* C,
+                              float* mask, int M, int N, int K, int Nbatch, int act) {
+    return guarded([&] {
+        return sync_after(matmul_bias_act_impl(A, B, bias, C, mask, M, N, K, Nbatch, act, nullptr));
+    });
+}
+
+int seera_hip_bias_grad_async(const float* dY, float* db, int rows, int N, void* stream) {
+    return guarded([&] { return queued(bias_grad_impl(dY, db, rows, N, as_stream(stream))); });
+}
+int seera_hip_bias_grad(const float* dY, float* db, int rows, int N) {
+    return guarded([&] { return sync_after(bias_grad_impl(dY, db, rows, N, nullptr)); });
 }
 
 int seera_hip_transpose_2d(const float* in, float* out, int rows, int cols) {

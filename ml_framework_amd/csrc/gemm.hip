@@ -26,7 +26,11 @@ struct Operand {
                                              StageMNC<ROWS, BK, NT, VEC>>::type;
 };
 
-template <bool A_KC, int VA, bool B_KC, int VB>
+// EPI: the fused forward epilogue (seera_hip_matmul_bias_act) applies
+// C = act(A.B + bias[n]) as each element is stored, and for ReLU also writes
+// mask = (pre-activation > 0); under split-K the partials are stored raw and
+// splitk_reduce_epi applies it after the sum.
+template <bool A_KC, int VA, bool B_KC, int VB, bool EPI = false>
 struct GemmProblem {
     const float* A;
     const float* B;
@@ -35,6 +39,10 @@ struct GemmProblem {
     int64_t lda, ldb, ldc;
     int64_t split_stride;  // distance between split-K partial outputs
     int tiles_n, k_split, gm;
+    const float* bias;     // EPI: [N] or nullptr
+    float* mask;           // EPI, act == kActRelu: [M, ldc] or nullptr
+    int act;               // EPI: kActNone or kActRelu
+    static constexpr bool kEpi = EPI;
 
     template <int R, int BK, int NT>
     using SA = typename Operand<A_KC, VA>::template Stager<R, BK, NT>;
@@ -69,7 +77,14 @@ struct GemmProblem {
     template <class S>
     __device__ __forceinline__ void init_b(S&, int, int) const {}
     __device__ __forceinline__ void store(int m, int n, int z, float v) const {
-        C[z * split_stride + (int64_t)m * ldc + n] = v;
+        const int64_t i = z * split_stride + (int64_t)m * ldc + n;
+        if constexpr (EPI) {
+            if (split_stride == 0) {  // whole K in this block: finish the element here
+                epilogue(C + i, mask ? mask + i : nullptr, v, bias ? bias[n] : 0.f, act);
+                return;
+            }
+        }
+        C[i] = v;
     }
 };
 
@@ -82,15 +97,29 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 // Dispatch on operand vector-load eligibility. Only the 64x64 tile carries the
 // scalar (any shape / alignment) variants.
-template <bool A_KC, bool B_KC>
+// Optional fused forward epilogue of gemm_dispatch<..., true>.
+struct Epi {
+    const float* bias = nullptr;
+    float* mask = nullptr;
+    int act = kActNone;
+};
+
+template <bool A_KC, bool B_KC, bool EPI = false>
 int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
-                  int64_t ldc, int M, int N, int K, hipStream_t st) {
+                  int64_t ldc, int M, int N, int K, hipStream_t st, Epi epi = Epi{}) {
     if (M == 0 || N == 0) return SEERA_OK;
     if (K == 0) {
-        // Empty contraction: C = 0 (the reference's K loop never runs).
+        // Empty contraction: C = 0 (the reference's K loop never runs), then
+        // the epilogue of a zero sum.
         const int64_t n = (int64_t)M * N;
-        hipLaunchKernelGGL(fill_zero_2d, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           C, M, N, ldc);
+        if constexpr (EPI) {
+            hipLaunchKernelGGL(splitk_reduce_epi, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                               st, (const float*)nullptr, C, M, N, ldc, 0, (int64_t)0, epi.bias,
+                               epi.mask, epi.act);
+        } else {
+            hipLaunchKernelGGL(fill_zero_2d, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               C, M, N, ldc);
+        }
         SEERA_HIP_TRY(hipGetLastError());
         return SEERA_OK;
     }
@@ -114,12 +143,13 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
         prob.M = M; prob.N = N; prob.K = K;
         prob.lda = lda; prob.ldb = ldb; prob.ldc = ldc;
         prob.split_stride = 0;
+        prob.bias = epi.bias; prob.mask = epi.mask; prob.act = epi.act;
         return prob;
     };
-    if (va && vb) return run_plan<true>(fill(GemmProblem<A_KC, 4, B_KC, 4>{}), pl, st);
-    if (va) return run_plan<false>(fill(GemmProblem<A_KC, 4, B_KC, 1>{}), pl, st);
-    if (vb) return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 4>{}), pl, st);
-    return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1>{}), pl, st);
+    if (va && vb) return run_plan<true>(fill(GemmProblem<A_KC, 4, B_KC, 4, EPI>{}), pl, st);
+    if (va) return run_plan<false>(fill(GemmProblem<A_KC, 4, B_KC, 1, EPI>{}), pl, st);
+    if (vb) return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 4, EPI>{}), pl, st);
+    return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1, EPI>{}), pl, st);
 }
 
 // LDS-tiled transpose of one [rows, cols] slice per blockIdx.z; 64x64 tiles,
@@ -152,6 +182,47 @@ int gemm_fwd(const float* A, const float* B, float* C, int M, int N, int K, int 
     if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
     // A [Mb, K] row-major (K-contiguous), B [K, N] row-major (N-contiguous).
     return gemm_dispatch<true, false>(A, K, B, N, C, N, (int)Mb, N, K, st);
+}
+
+int gemm_fwd_bias_act(const float* A, const float* B, const float* bias, float* C, float* mask,
+                      int M, int N, int K, int Nbatch, int act, hipStream_t st) {
+    const int64_t Mb = (int64_t)M * Nbatch;
+    if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    Epi e;
+    e.bias = bias;
+    e.mask = mask;
+    e.act = act;
+    return gemm_dispatch<true, false, true>(A, K, B, N, C, N, (int)Mb, N, K, st, e);
+}
+
+// db[n] = sum over rows of dY[row, n]: fixed-order partial sums of the rows a
+// thread group owns, added in group order (bit-reproducible run to run).
+constexpr int kBgCols = 64, kBgGroups = 8;
+__global__ __launch_bounds__(kBgCols * kBgGroups) void bias_grad_kernel(
+    const float* __restrict__ dY, float* __restrict__ db, int rows, int N) {
+    __shared__ float part[kBgGroups][kBgCols];
+    const int col = threadIdx.x % kBgCols, grp = threadIdx.x / kBgCols;
+    const int n = blockIdx.x * kBgCols + col;
+    const int per = (rows + kBgGroups - 1) / kBgGroups;
+    const int r0 = grp * per, r1 = min(rows, r0 + per);
+    float s = 0.f;
+    if (n < N)
+        for (int r = r0; r < r1; ++r) s += dY[(int64_t)r * N + n];
+    part[grp][col] = s;
+    __syncthreads();
+    if (grp != 0 || n >= N) return;
+    float t = part[0][col];
+#pragma unroll
+    for (int g = 1; g < kBgGroups; ++g) t += part[g][col];
+    db[n] = t;
+}
+
+int bias_grad(const float* dY, float* db, int rows, int N, hipStream_t st) {
+    if (N == 0) return SEERA_OK;
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((unsigned)((N + kBgCols - 1) / kBgCols)),
+                       dim3(kBgCols * kBgGroups), 0, st, dY, db, rows, N);
+    SEERA_HIP_TRY(hipGetLastError());
+    return SEERA_OK;
 }
 
 int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M,

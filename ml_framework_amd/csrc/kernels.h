@@ -9,6 +9,12 @@ namespace seera {
 // C[Mb, N] = A[Mb, K] . B[K, N] with Mb = M * Nbatch.
 int gemm_fwd(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch,
              hipStream_t st);
+// C = act(A . B + bias[n]) (bias may be null; act: 0 none, 1 ReLU, which also
+// writes mask = pre-activation > 0 when mask is non-null).
+int gemm_fwd_bias_act(const float* A, const float* B, const float* bias, float* C, float* mask,
+                      int M, int N, int K, int Nbatch, int act, hipStream_t st);
+// db[n] = sum_r dY[r, n] for dY [rows, N].
+int bias_grad(const float* dY, float* db, int rows, int N, hipStream_t st);
 // dA = dC . B^T, dB = A^T . dC over the folded batch.
 int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M, int N,
              int K, int Nbatch, hipStream_t st);

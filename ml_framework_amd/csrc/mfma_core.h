@@ -322,6 +322,22 @@ struct WsStageMNC {
     }
 };
 
+// Fused forward epilogue (Dense layer: matmul, broadcast_add_4d, relu --
+// engine_cuda/src/broadcast.cu:12-64, activations.cu:9-15): the bias is added
+// in fp32 to the fp32 result, and ReLU writes out = v > 0 ? v : 0 and
+// mask = v > 0 ? 1 : 0, so the result is the unfused sequence's, bit for bit.
+constexpr int kActNone = 0, kActRelu = 1;
+__device__ __forceinline__ void epilogue(float* out, float* mask, float v, float bias, int act) {
+    v += bias;
+    if (act == kActRelu) {
+        const bool pos = v > 0.f;
+        *out = pos ? v : 0.f;
+        if (mask) *mask = pos ? 1.f : 0.f;
+    } else {
+        *out = v;
+    }
+}
+
 // Bytes a K-contiguous stager's resource must span for a ROWS x BK tile with
 // leading dimension ld (host-side check against kMaxTileSpanBytes).
 inline int64_t span_kc(int rows, int bk, int64_t ld) { return ((int64_t)rows * ld + bk) * 4; }

@@ -82,6 +82,26 @@ struct ws_stream : std::false_type {};
 template <class P>
 struct ws_stream<P, std::void_t<decltype(P::kWsStream)>> : std::bool_constant<P::kWsStream> {};
 
+// The same sum, then the fused forward epilogue (bias, activation, mask).
+static __global__ void splitk_reduce_epi(const float* __restrict__ P, float* __restrict__ C,
+                                         int M, int N, int64_t ldc, int splits, int64_t stride,
+                                         const float* __restrict__ bias, float* __restrict__ mask,
+                                         int act) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * N) return;
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += P[z * stride + i];
+    const int n = (int)(i % N);
+    const int64_t o = (i / N) * ldc + n;
+    epilogue(C + o, mask ? mask + o : nullptr, s, bias ? bias[n] : 0.f, act);
+}
+
+// Problems with a fused epilogue declare `static constexpr bool kEpi = true`.
+template <class P, class = void>
+struct has_epi : std::false_type {};
+template <class P>
+struct has_epi<P, std::void_t<decltype(P::kEpi)>> : std::bool_constant<P::kEpi> {};
+
 template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
     if constexpr (BIG) {
@@ -124,8 +144,14 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
     if (e != hipSuccess) return fail_hip(e, "igemm launch");
     if (pl.splits > 1) {
         const int64_t n = (int64_t)p.M * p.N;
-        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride);
+        if constexpr (has_epi<P>::value) {
+            hipLaunchKernelGGL(splitk_reduce_epi, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                               st, p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride,
+                               p.bias, p.mask, p.act);
+        } else {
+            hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride);
+        }
         SEERA_HIP_TRY(hipGetLastError());
     }
     return SEERA_OK;

@@ -1,0 +1,102 @@
+"""Fused Dense-layer forward (matmul + bias + ReLU in the GEMM's store) and
+the bias gradient. The reference runs the forward as cuda_matmul,
+broadcast_add_4d and cuda_relu_fwd (GEMM.cu:95-103, broadcast.cu:12-64,
+activations.cu:9-15); the fused entry point must equal that sequence bit for
+bit, which is checked against the unfused GPU GEMM with the fp32 bias add and
+ReLU done in numpy. db is the reference's Reductionsum over the batch
+(reductionKernels.cu:12-29; Seera_Engine.py:43-65)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from ml_framework_amd import capi
+from ml_framework_amd.capi import DeviceBuffer, check, load
+from tests.helpers import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _gpu():
+    assert capi.gpu_available(), "no HIP device visible"
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+SHAPES = [
+    (256, 784, 512, 1),    # MLP cfg3 layer 1
+    (256, 512, 256, 1),    # layer 2
+    (256, 256, 10, 1),     # layer 3 (N = 10 edge tile)
+    (64, 2048, 64, 1),     # few tiles: split-K, epilogue in the reduce
+    (33, 65, 17, 2),       # odd dims, folded batch
+    (7, 0, 5, 1),          # K = 0: C = act(bias)
+    (4096, 4096, 512, 1),  # 256x256 warp-specialised tiles
+]
+
+
+@pytest.mark.parametrize("M,K,N,nb", SHAPES)
+@pytest.mark.parametrize("act", [capi.SEERA_ACT_NONE, capi.SEERA_ACT_RELU])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fused_bias_act_equals_unfused(M, K, N, nb, act, with_bias):
+    r = np.random.default_rng(M * 31 + K * 7 + N + act)
+    a = r.uniform(-1, 1, (nb, M, K)).astype(np.float32)
+    b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = r.uniform(-1, 1, N).astype(np.float32)
+    lib = load()
+    with DeviceBuffer.from_array(a if a.size else np.zeros(1, np.float32)) as A, \
+            DeviceBuffer.from_array(b if b.size else np.zeros(1, np.float32)) as B, \
+            DeviceBuffer.from_array(bias) as Bi, DeviceBuffer(nb * M * N * 4) as C0, \
+            DeviceBuffer(nb * M * N * 4) as C, DeviceBuffer(nb * M * N * 4) as Mk:
+        check(lib.seera_hip_matmul(A.ptr, B.ptr, C0.ptr, M, N, K, nb))
+        Mk.fill(0x7F)
+        check(lib.seera_hip_matmul_bias_act(A.ptr, B.ptr, Bi.ptr if with_bias else None, C.ptr,
+                                            Mk.ptr, M, N, K, nb, act))
+        plain = C0.to_array((nb, M, N))
+        pre = plain + (bias if with_bias else np.float32(0))
+        want = np.where(pre > 0, pre, np.float32(0)) if act == capi.SEERA_ACT_RELU else pre
+        got = C.to_array((nb, M, N))
+        assert np.array_equal(_bits(got), _bits(want))
+        mask = Mk.to_array((nb, M, N))
+        if act == capi.SEERA_ACT_RELU:
+            assert np.array_equal(mask, (pre > 0).astype(np.float32))
+        else:  # mask untouched without ReLU
+            assert (_bits(mask) == 0x7F7F7F7F).all()
+
+
+def test_relu_mask_optional():
+    r = np.random.default_rng(3)
+    a = r.uniform(-1, 1, (64, 96)).astype(np.float32)
+    b = r.uniform(-1, 1, (96, 48)).astype(np.float32)
+    lib = load()
+    with DeviceBuffer.from_array(a) as A, DeviceBuffer.from_array(b) as B, \
+            DeviceBuffer(64 * 48 * 4) as C0, DeviceBuffer(64 * 48 * 4) as C:
+        check(lib.seera_hip_matmul(A.ptr, B.ptr, C0.ptr, 64, 48, 96, 1))
+        check(lib.seera_hip_matmul_bias_act(A.ptr, B.ptr, None, C.ptr, None, 64, 48, 96, 1,
+                                            capi.SEERA_ACT_RELU))
+        plain = C0.to_array((64, 48))
+        assert np.array_equal(_bits(C.to_array((64, 48))), _bits(np.maximum(plain, 0)))
+
+
+def test_unknown_activation_is_rejected():
+    st = load().seera_hip_matmul_bias_act(None, None, None, None, None, 1, 1, 1, 1, 7)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT
+    assert "activation" in load().seera_hip_last_error().decode()
+
+
+@pytest.mark.parametrize("rows,N", [(256, 10), (256, 512), (1, 3), (1000, 65), (65536, 128), (5, 0)])
+def test_bias_grad(rows, N):
+    r = np.random.default_rng(rows + N)
+    dy = r.standard_normal((rows, N)).astype(np.float32)
+    lib = load()
+    with DeviceBuffer.from_array(dy if dy.size else np.zeros(1, np.float32)) as D, \
+            DeviceBuffer(max(N, 1) * 4) as db1, DeviceBuffer(max(N, 1) * 4) as db2:
+        check(lib.seera_hip_bias_grad(D.ptr, db1.ptr, rows, N))
+        check(lib.seera_hip_bias_grad(D.ptr, db2.ptr, rows, N))
+        g1, g2 = db1.to_array((N,)), db2.to_array((N,))
+        assert np.array_equal(_bits(g1), _bits(g2))  # fixed summation order
+        ref = dy.astype(np.float64).sum(axis=0)
+        # fp32 sums of up to rows/8 terms per group: the error grows with rows
+        assert_parity(g1, ref, "db", rel=1e-5, mabs=max(1e-4, rows * 1e-7))
