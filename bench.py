@@ -9,7 +9,8 @@ synchronize on both sides.
 
 Also reported (same run, fewer repetitions): GEMM fwd+bwd at 4096^3, Conv2D
 3x3 fwd+bwd (config 4), ConvTranspose2D 4x4 s2 fwd+bwd (config 5), the
-MLP 784-512-256-10 GEMMs (config 3), and the CPU baseline (the oracle's
+MLP 784-512-256-10 GEMMs (config 3), MaxPool2D over config 4's activation,
+and the CPU baseline (the oracle's
 restatement of seera_cpp on OpenBLAS, on this host's cores).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
@@ -150,6 +151,39 @@ def bench_convT(steps, warmup, stream):
     for v in (px, pw, pdy, py, pdx, pdw):
         v.close()
     return res
+
+
+def bench_maxpool(steps, warmup, stream, K, s, p):
+    """MaxPool2D KxK stride s pad p over config 4's activation [128, 64, 56, 56]
+    (the layer after the conv in the reference's CNNs); fwd (out + mask) and
+    bwd (dX). Algorithmic HBM bytes per pass: x or dX (4 B per input), mask
+    (4 B per input), out or dout (4 B per output)."""
+    r = np.random.default_rng(0)
+    N, C, H, W = 128, 64, 56, 56
+    Ho, Wo = (H + 2 * p - K) // s + 1, (W + 2 * p - K) // s + 1
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    dout = r.standard_normal((N, C, Ho, Wo)).astype(np.float32)
+    lib = capi.load()
+    px, pg = DeviceBuffer.from_array(x), DeviceBuffer.from_array(dout)
+    po, pm, pdx = DeviceBuffer(dout.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(x.nbytes)
+    args = (N, C, H, W, K, K, p, p, s, s)
+
+    def fwd():
+        capi.check(lib.seera_hip_maxpool_fwd_async(px.ptr, po.ptr, pm.ptr, *args, stream.ptr))
+
+    def bwd():
+        capi.check(lib.seera_hip_maxpool_bwd_async(pg.ptr, pm.ptr, pdx.ptr, *args, stream.ptr))
+
+    ms_f, ms_b = timed(fwd, steps, warmup, stream), timed(bwd, steps, warmup, stream)
+    nbytes = 4 * (2 * x.size + dout.size)
+    for v in (px, pg, po, pm, pdx):
+        v.close()
+    return {"shape": f"[{N},{C},{H},{W}] {K}x{K} s{s} p{p}", "ms_fwd": round(ms_f, 5),
+            "ms_bwd": round(ms_b, 5), "bytes_per_pass": nbytes,
+            "fwd_gbs": round(nbytes / (ms_f * 1e-3) / 1e9, 1),
+            "bwd_gbs": round(nbytes / (ms_b * 1e-3) / 1e9, 1),
+            "fwd_frac_hbm": round(nbytes / (ms_f * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "bwd_frac_hbm": round(nbytes / (ms_b * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
 
 
 def bench_mlp(steps, warmup, stream):
@@ -335,6 +369,8 @@ def main():
             "fwd_bwd_tflops": round(ct_flops / ((ct["ms_fwd"] + ct["ms_bwd"]) * 1e-3) / 1e12, 2),
         }
         extras["mlp_cfg3"] = {k: round(v, 4) for k, v in bench_mlp(20, 3, stream).items()}
+        extras["maxpool_2x2_s2"] = bench_maxpool(20, 3, stream, 2, 2, 0)
+        extras["maxpool_3x3_s2_p1"] = bench_maxpool(20, 3, stream, 3, 2, 1)
         out["extras"] = extras
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(n)

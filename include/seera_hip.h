@@ -109,6 +109,32 @@ int seera_hip_bias_grad(const float *dY, float *db, int rows, int N);
 int seera_hip_bias_grad_async(const float *dY, float *db, int rows, int N,
                               void *stream);
 
+/* cuda_maxpool_fwd (maxPool.cu:9-53, 79-103; binding cuda_bindings.cpp:338-343):
+ * out [batchN, C, Ho, Wo] with Ho = (H + 2 pad_h - R) / stride_h + 1; mask
+ * [batchN, C, H, W] int32, 1 at each window's argmax and 0 elsewhere. The max
+ * starts at the window origin (0 if the origin is padding) and ties go to the
+ * later element, as in the reference; where windows overlap, an element that
+ * is any window's argmax is 1 (the reference leaves that to thread order). */
+int seera_hip_maxpool_fwd(const float *image, float *out, int *mask, int batchN,
+                          int C, int H, int W, int R, int S, int pad_h,
+                          int pad_w, int stride_h, int stride_w);
+/* cuda_maxpool_bwd (maxPool.cu:56-77, 105-129; binding cuda_bindings.cpp:346-351):
+ * dX [batchN, C, H, W] = sum over the windows covering each element of
+ * dout * mask (overwritten). */
+int seera_hip_maxpool_bwd(const float *dout, const int *mask, float *dX,
+                          int batchN, int C, int H, int W, int R, int S,
+                          int pad_h, int pad_w, int stride_h, int stride_w);
+/* The same two on `stream`, returning once queued (as the other _async
+ * entry points). */
+int seera_hip_maxpool_fwd_async(const float *image, float *out, int *mask,
+                                int batchN, int C, int H, int W, int R, int S,
+                                int pad_h, int pad_w, int stride_h,
+                                int stride_w, void *stream);
+int seera_hip_maxpool_bwd_async(const float *dout, const int *mask, float *dX,
+                                int batchN, int C, int H, int W, int R, int S,
+                                int pad_h, int pad_w, int stride_h,
+                                int stride_w, void *stream);
+
 /* cuda_transpose_2d (GEMM.cu:229-235; binding cuda_bindings.cpp:276-280).
  * out[c,r] = in[r,c], bit-exact. */
 int seera_hip_transpose_2d(const float *in, float *out, int rows, int cols);

@@ -44,6 +44,10 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_matmul_bias_act": ([_vp] * 5 + [_i] * 5, _i),
     "seera_hip_matmul_bias_act_async": ([_vp] * 5 + [_i] * 5 + [_vp], _i),
     "seera_hip_bias_grad": ([_vp, _vp, _i, _i], _i),
+    "seera_hip_maxpool_fwd": ([_vp] * 3 + [_i] * 10, _i),
+    "seera_hip_maxpool_bwd": ([_vp] * 3 + [_i] * 10, _i),
+    "seera_hip_maxpool_fwd_async": ([_vp] * 3 + [_i] * 10 + [_vp], _i),
+    "seera_hip_maxpool_bwd_async": ([_vp] * 3 + [_i] * 10 + [_vp], _i),
     "seera_hip_bias_grad_async": ([_vp, _vp, _i, _i, _vp], _i),
     "seera_hip_matmul_bwd": ([_vp] * 5 + [_i] * 4, _i),
     "seera_hip_matmul_bwd_async": ([_vp] * 5 + [_i] * 4 + [_vp], _i),

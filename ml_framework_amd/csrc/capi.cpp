@@ -81,6 +81,34 @@ int bias_grad_impl(const float* dY, float* db, int rows, int N, hipStream_t st) 
     SEERA_TRY(check_ptrs(N > 0, db, rows > 0 ? dY : db, db));
     return bias_grad(dY, db, rows, N, st);
 }
+int pool_dims(int B, int C, int H, int W, int R, int S, int ph, int pw, int sh, int sw) {
+    SEERA_TRY(check_conv_geometry(R, S, sh, sw, ph, pw));
+    if (B < 0 || C < 1 || H < 1 || W < 1)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "maxpool: bad tensor dims");
+    // Keeps h * sh + R and H + 2 * ph (and the W counterparts) inside int.
+    constexpr int kMaxExtent = 1 << 20;
+    if (H > kMaxExtent || W > kMaxExtent || R > kMaxExtent || S > kMaxExtent ||
+        ph > kMaxExtent || pw > kMaxExtent || sh > kMaxExtent || sw > kMaxExtent)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "maxpool: extent, pad or stride above 2^20");
+    if (H + 2 * ph < R || W + 2 * pw < S)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "maxpool: window larger than padded input");
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    if (prod(B, C, H, W) > INT_MAX || prod(B, C, Ho, Wo) > INT_MAX)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "maxpool: tensor exceeds int range");
+    return SEERA_OK;
+}
+int maxpool_fwd_impl(const float* x, float* out, int* mask, int B, int C, int H, int W, int R,
+                     int S, int ph, int pw, int sh, int sw, hipStream_t st) {
+    SEERA_TRY(pool_dims(B, C, H, W, R, S, ph, pw, sh, sw));
+    SEERA_TRY(check_ptrs(B > 0, x, out, mask));
+    return maxpool_fwd(x, out, mask, B, C, H, W, R, S, ph, pw, sh, sw, st);
+}
+int maxpool_bwd_impl(const float* dout, const int* mask, float* dx, int B, int C, int H, int W,
+                     int R, int S, int ph, int pw, int sh, int sw, hipStream_t st) {
+    SEERA_TRY(pool_dims(B, C, H, W, R, S, ph, pw, sh, sw));
+    SEERA_TRY(check_ptrs(B > 0, dout, mask, dx));
+    return maxpool_bwd(dout, mask, dx, B, C, H, W, R, S, ph, pw, sh, sw, st);
+}
 int matmul_bwd_impl(const float* A, const float* B, const float* dC, float* dA, float* dB, int M,
                     int N, int K, int Nbatch, hipStream_t st) {
     if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
@@ -288,6 +316,37 @@ int seera_hip_bias_grad_async(const float* dY, float* db, int rows, int N, void*
 }
 int seera_hip_bias_grad(const float* dY, float* db, int rows, int N) {
     return guarded([&] { return sync_after(bias_grad_impl(dY, db, rows, N, nullptr)); });
+}
+
+int seera_hip_maxpool_fwd(const float* image, float* out, int* mask, int batchN, int C, int H,
+                          int W, int R, int S, int pad_h, int pad_w, int stride_h, int stride_w) {
+    return guarded([&] {
+        return sync_after(maxpool_fwd_impl(image, out, mask, batchN, C, H, W, R, S, pad_h, pad_w,
+                                           stride_h, stride_w, nullptr));
+    });
+}
+int seera_hip_maxpool_bwd(const float* dout, const int* mask, float* dX, int batchN, int C, int H,
+                          int W, int R, int S, int pad_h, int pad_w, int stride_h, int stride_w) {
+    return guarded([&] {
+        return sync_after(maxpool_bwd_impl(dout, mask, dX, batchN, C, H, W, R, S, pad_h, pad_w,
+                                           stride_h, stride_w, nullptr));
+    });
+}
+int seera_hip_maxpool_fwd_async(const float* image, float* out, int* mask, int batchN, int C,
+                                int H, int W, int R, int S, int pad_h, int pad_w, int stride_h,
+                                int stride_w, void* stream) {
+    return guarded([&] {
+        return queued(maxpool_fwd_impl(image, out, mask, batchN, C, H, W, R, S, pad_h, pad_w,
+                                       stride_h, stride_w, as_stream(stream)));
+    });
+}
+int seera_hip_maxpool_bwd_async(const float* dout, const int* mask, float* dX, int batchN, int C,
+                                int H, int W, int R, int S, int pad_h, int pad_w, int stride_h,
+                                int stride_w, void* stream) {
+    return guarded([&] {
+        return queued(maxpool_bwd_impl(dout, mask, dX, batchN, C, H, W, R, S, pad_h, pad_w,
+                                       stride_h, stride_w, as_stream(stream)));
+    });
 }
 
 int seera_hip_transpose_2d(const float* in, float* out, int rows, int cols) {

@@ -21,6 +21,13 @@ int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* 
 // out[b, c, r] = in[b, r, c] for b < batch.
 int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st);
 
+// MaxPool2D with the reference GPU engine's semantics (pool.hip): out
+// [B, C, Ho, Wo], mask [B, C, H, W] int32 0/1; dX = mask * sum of covering dout.
+int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int W, int R, int S,
+                int ph, int pw, int sh, int sw, hipStream_t st);
+int maxpool_bwd(const float* dout, const int* mask, float* dx, int B, int C, int H, int W, int R,
+                int S, int ph, int pw, int sh, int sw, hipStream_t st);
+
 // p[0, n) = v.
 int fill_f32(float* p, float v, size_t n, hipStream_t st);
 

@@ -115,6 +115,22 @@ PYBIND11_MODULE(seera_cuda, m) {
               return p;
           },
           "Allocate total_elements floats filled with 0 (GPU ptr)");
+    // cuda_bindings.cpp:338-351 (mask: int32 [batchN, C, H, W], as cuTen.py:592 allocates it).
+    m.def("cuda_maxpool_fwd",
+          [](uintptr_t image, uintptr_t out, uintptr_t mask, int batchN, int C, int H, int W,
+             int R, int S, int pad_h, int pad_w, int stride_h, int stride_w) {
+              check(seera_hip_maxpool_fwd(dev<const float>(image), dev<float>(out), dev<int>(mask),
+                                          batchN, C, H, W, R, S, pad_h, pad_w, stride_h, stride_w));
+          },
+          "MaxPool2D forward (GPU ptrs, mask int32 [N, C, H, W])");
+    m.def("cuda_maxpool_bwd",
+          [](uintptr_t dout, uintptr_t mask, uintptr_t dX, int batchN, int C, int H, int W, int R,
+             int S, int pad_h, int pad_w, int stride_h, int stride_w) {
+              check(seera_hip_maxpool_bwd(dev<const float>(dout), dev<const int>(mask),
+                                          dev<float>(dX), batchN, C, H, W, R, S, pad_h, pad_w,
+                                          stride_h, stride_w));
+          },
+          "MaxPool2D backward (GPU ptrs)");
     // Not in the reference: the caching allocator behind cuda_malloc / cuda_free.
     m.def("cuda_empty_cache", []() { check(seera_hip_empty_cache()); },
           "Return the allocator's cached blocks to HIP");

@@ -95,3 +95,30 @@ MATMUL = [
     # Dense 64x784x128
     (64, 784, 128, 1),
 ]
+
+# Testing/test_1.py:309-340 -- (name, N, C, H, W, KH, KW, stride, pad), MaxPool2D
+MAXPOOL = [
+    ("p01", 2, 4, 8, 8, 2, 2, 2, 0),
+    ("p02", 2, 4, 9, 9, 3, 3, 3, 0),
+    ("p03", 2, 4, 16, 16, 4, 4, 4, 0),
+    ("p04", 2, 4, 8, 8, 2, 2, 1, 0),
+    ("p05", 2, 4, 8, 8, 3, 3, 2, 0),
+    ("p06", 2, 4, 8, 8, 3, 3, 1, 0),
+    ("p07", 2, 4, 8, 8, 2, 2, 2, 1),
+    ("p08", 2, 4, 8, 8, 3, 3, 2, 1),
+    ("p09", 1, 8, 8, 8, 2, 2, 2, 0),
+    ("p10", 16, 8, 8, 8, 2, 2, 2, 0),
+    ("p11", 2, 64, 8, 8, 2, 2, 2, 0),
+    ("p12", 2, 1, 8, 8, 2, 2, 2, 0),
+    ("p13", 2, 4, 4, 16, 2, 2, 2, 0),
+    ("p14", 2, 4, 16, 4, 2, 2, 2, 0),
+    ("p15", 2, 4, 32, 32, 2, 2, 2, 0),
+    ("p16", 2, 4, 64, 64, 4, 4, 4, 0),
+    ("p17", 4, 8, 4, 4, 4, 4, 4, 0),
+    # not from the reference's tests: stride > kernel (gaps), padding >= the
+    # window (windows wholly in the padding), an odd extent that the stride
+    # does not divide
+    ("q01", 2, 3, 11, 11, 2, 2, 3, 0),
+    ("q02", 1, 2, 5, 7, 2, 2, 1, 2),
+    ("q03", 2, 3, 13, 10, 3, 3, 2, 1),
+]

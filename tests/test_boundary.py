@@ -80,6 +80,8 @@ REFERENCE_SIGNATURES = {
     "cuda_conv2DTranspose_bwd": 16,      # 324
     "cuda_ones_f": 1,                    # 467 (total_elements) -> device pointer
     "cuda_zeros_f": 1,                   # 474 (total_elements) -> device pointer
+    "cuda_maxpool_fwd": 13,              # 338 (image, out, mask, N, C, H, W, R, S, ph, pw, sh, sw)
+    "cuda_maxpool_bwd": 13,              # 346 (dout, mask, dX, N, C, H, W, R, S, ph, pw, sh, sw)
 }
 
 
@@ -140,3 +142,16 @@ def test_no_device_is_a_clean_error():
     p = ctypes.c_void_p()
     st = capi.load().seera_hip_malloc(ctypes.byref(p), 1024)
     assert st != capi.SEERA_OK and capi.load().seera_hip_last_error()
+
+
+@pytest.mark.parametrize("args,what", [
+    ((2, 3, 8, 8, 2, 2, 0, 0, 0, 2), "stride"),          # stride_h = 0
+    ((2, 3, 8, 8, 2, 2, -1, 0, 2, 2), "padding"),        # pad_h < 0
+    ((2, 3, 2, 8, 5, 2, 1, 0, 1, 1), "larger"),          # R > H + 2 pad
+    ((2, 0, 8, 8, 2, 2, 0, 0, 2, 2), "dims"),            # C = 0
+    ((1, 1, 8, 8, 2, 2, 1 << 21, 0, 1, 1), "2^20"),      # pad near int overflow
+])
+def test_validation_maxpool(args, what):
+    for name in ("seera_hip_maxpool_fwd", "seera_hip_maxpool_bwd"):
+        st, msg = _status(name, 1, 1, 1, *args)
+        assert st == capi.SEERA_ERR_INVALID_ARGUMENT and what in msg, (name, msg)

@@ -111,3 +111,29 @@ def test_memory_helpers(sc):
 def test_errors_raise(sc):
     with pytest.raises(RuntimeError, match="stride"):
         sc.cuda_conv2d_fwd(0, 0, 0, 1, 3, 8, 8, 4, 3, 3, 1, 1, 0, 1)
+
+
+def test_maxpool_call_sequence(sc):
+    """cuTen.maxpool2d (cuTen.py:578-606): cuda_malloc_f32 the output,
+    cuda_malloc_i32 the mask, cuda_maxpool_fwd; Seera_Engine.py:117-136:
+    cuda_malloc_f32 + cuda_memset dX, cuda_maxpool_bwd."""
+    from oracle import pool
+
+    r = np.random.default_rng(6)
+    N, C, H, W, K, s, p = 2, 3, 9, 8, 3, 2, 1
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    OH, OW = 5, 4
+    px = sc.to_device_f32(x)
+    pout, pmask = sc.cuda_malloc_f32(N * C * OH * OW), sc.cuda_malloc_i32(x.size)
+    sc.cuda_maxpool_fwd(px, pout, pmask, N, C, H, W, K, K, p, p, s, s)
+    ro, rm = pool.maxpool_fwd(x, K, K, p, p, s, s)
+    assert np.array_equal(sc.to_host_f32(pout, (N, C, OH, OW)), ro)
+    assert np.array_equal(sc.to_host_i32(pmask, x.shape), rm)
+    dout = r.standard_normal((N, C, OH, OW)).astype(np.float32)
+    pg = sc.to_device_f32(dout)
+    pdx = sc.cuda_malloc_f32(x.size)
+    sc.cuda_memset(pdx, 0, x.size * 4)
+    sc.cuda_maxpool_bwd(pg, pmask, pdx, N, C, H, W, K, K, p, p, s, s)
+    assert np.array_equal(sc.to_host_f32(pdx, x.shape), pool.maxpool_bwd(dout, rm, K, K, p, p, s, s))
+    for q in (px, pout, pmask, pg, pdx):
+        sc.cuda_free(q)
