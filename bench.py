@@ -120,8 +120,23 @@ def bench_conv(steps, warmup, stream):
         capi.check(lib.seera_hip_conv2d_bwd_async(pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr, N, C,
                                                   H, W, F, 3, 3, 1, 1, 1, 1, stream.ptr))
 
-    res = {"ms_fwd": timed(fwd, steps, warmup, stream), "ms_bwd": timed(bwd, steps, warmup, stream)}
-    for v in (px, pw, pdy, py, pdx, pdw):
+    # The Conv2D layer forward with its bias and ReLU (and mask) in the conv's
+    # store, and the bias gradient (a fixed-order sum of dY per channel).
+    pb = DeviceBuffer.from_array(r.uniform(-0.1, 0.1, F).astype(np.float32))
+    pm, pdb = DeviceBuffer(x.nbytes), DeviceBuffer(F * 4)
+
+    def fwd_fused():
+        capi.check(lib.seera_hip_conv2d_fwd_bias_act_async(
+            px.ptr, pw.ptr, pb.ptr, py.ptr, pm.ptr, N, C, H, W, F, 3, 3, 1, 1, 1, 1,
+            capi.SEERA_ACT_RELU, stream.ptr))
+
+    def bias_grad():
+        capi.check(lib.seera_hip_conv_bias_grad_async(pdy.ptr, pdb.ptr, N, F, H * W, stream.ptr))
+
+    res = {"ms_fwd": timed(fwd, steps, warmup, stream), "ms_bwd": timed(bwd, steps, warmup, stream),
+           "ms_fwd_fused_bias_relu": timed(fwd_fused, steps, warmup, stream),
+           "ms_bias_grad": timed(bias_grad, steps, warmup, stream)}
+    for v in (px, pw, pdy, py, pdx, pdw, pb, pm, pdb):
         v.close()
     return res
 
@@ -358,6 +373,8 @@ def main():
         conv_flops = 29.6e9 * 3  # 2*N*F*Ho*Wo*C*R*S per pass, 3 passes
         extras["conv2d_cfg4"] = {
             "ms_fwd": round(cv["ms_fwd"], 4), "ms_bwd": round(cv["ms_bwd"], 4),
+            "ms_fwd_fused_bias_relu": round(cv["ms_fwd_fused_bias_relu"], 4),
+            "ms_bias_grad": round(cv["ms_bias_grad"], 4),
             "fwd_bwd_tflops": round(conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3) / 1e12, 2),
             "pct_mfma_peak": round(100 * conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3)
                                    / 1e12 / PEAK_FP16_TFLOPS, 2),

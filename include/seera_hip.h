@@ -160,6 +160,36 @@ int seera_hip_conv2d_fwd_async(const float *image, const float *kernel,
                                int N, int R, int S, int pad_h, int pad_w,
                                int stride_h, int stride_w, void *stream);
 
+/* No single counterpart in the reference: a Conv2D layer's forward
+ * (Seera.py:254-257) runs cuda_conv2d_fwd (convolution.cu:367-389), then
+ * broadcast_add_4d of the bias [1, N, 1, 1] (broadcast.cu:12-64, 140-146),
+ * then cuda_relu_fwd (activations.cu:9-15). Here the bias (NULL: none) and
+ * act (SEERA_ACT_NONE or SEERA_ACT_RELU) are applied in the convolution's
+ * store: conv = act(conv2d(image, kernel) + bias[n]), and with ReLU and a
+ * non-NULL mask, mask = v > 0 ? 1 : 0, [batchN, N, Hout, Wout] like conv.
+ * Bit-identical to the three calls. Argument order as seera_hip_conv2d_fwd. */
+int seera_hip_conv2d_fwd_bias_act(const float *image, const float *kernel,
+                                  const float *bias, float *conv, float *mask,
+                                  int batchN, int C, int H, int W, int N, int R,
+                                  int S, int pad_h, int pad_w, int stride_h,
+                                  int stride_w, int act);
+int seera_hip_conv2d_fwd_bias_act_async(const float *image, const float *kernel,
+                                        const float *bias, float *conv,
+                                        float *mask, int batchN, int C, int H,
+                                        int W, int N, int R, int S, int pad_h,
+                                        int pad_w, int stride_h, int stride_w,
+                                        int act, void *stream);
+
+/* The Conv2D bias gradient: the reference reduces dY [batchN, N, H, W] to the
+ * bias shape [1, N, 1, 1] with three sums (Seera_Engine.py:42-65, cuTen sum
+ * over axes 3, 2, 0; reductionKernels.cu:12-29). Here db[n] = sum over images
+ * and the HW pixels of dY in one fixed order (deterministic; fp32 sums in
+ * another order than the reference's). */
+int seera_hip_conv_bias_grad(const float *dY, float *db, int batchN, int N,
+                             int HW);
+int seera_hip_conv_bias_grad_async(const float *dY, float *db, int batchN,
+                                   int N, int HW, void *stream);
+
 /* cuda_conv2d_bwd (convolution.cu:393-453; binding cuda_bindings.cpp:302-309).
  * NOTE the argument order: stride before pad.
  * dX = adjoint of conv2d_fwd in the image, dW = adjoint in the kernel. */

@@ -54,6 +54,10 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_transpose_2d": ([_vp, _vp, _i, _i], _i),
     "seera_hip_transpose_3d": ([_vp, _vp, _i, _i, _i], _i),
     "seera_hip_conv2d_fwd": (_conv14, _i),
+    "seera_hip_conv2d_fwd_bias_act": ([_vp] * 5 + [_i] * 12, _i),
+    "seera_hip_conv2d_fwd_bias_act_async": ([_vp] * 5 + [_i] * 12 + [_vp], _i),
+    "seera_hip_conv_bias_grad": ([_vp, _vp, _i, _i, _i], _i),
+    "seera_hip_conv_bias_grad_async": ([_vp, _vp, _i, _i, _i, _vp], _i),
     "seera_hip_conv2d_fwd_async": (_conv14 + [_vp], _i),
     "seera_hip_conv2d_bwd": (_conv16, _i),
     "seera_hip_conv2d_bwd_async": (_conv16 + [_vp], _i),

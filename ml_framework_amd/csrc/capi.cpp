@@ -130,6 +130,29 @@ int conv2d_fwd_impl(const float* image, const float* kernel, float* conv, int ba
     return conv_fwd(image, kernel, conv, batchN, C, H, W, N, R, S, stride_h, stride_w, pad_h, pad_w,
                     st);
 }
+int conv2d_fwd_bias_act_impl(const float* image, const float* kernel, const float* bias,
+                             float* conv, float* mask, int batchN, int C, int H, int W, int N,
+                             int R, int S, int pad_h, int pad_w, int stride_h, int stride_w,
+                             int act, hipStream_t st) {
+    SEERA_TRY(check_conv_geometry(R, S, stride_h, stride_w, pad_h, pad_w));
+    if (batchN < 0 || C < 1 || H < 1 || W < 1 || N < 1)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_fwd: bad tensor dims");
+    if (H + 2 * pad_h < R || W + 2 * pad_w < S)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_fwd: kernel larger than padded input");
+    if (act != SEERA_ACT_NONE && act != SEERA_ACT_RELU)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "unknown activation %d", act);
+    SEERA_TRY(check_ptrs(batchN > 0, image, kernel, conv));
+    return conv_fwd_bias_act(image, kernel, bias, conv, act == SEERA_ACT_RELU ? mask : nullptr,
+                             batchN, C, H, W, N, R, S, stride_h, stride_w, pad_h, pad_w, act, st);
+}
+int conv_bias_grad_impl(const float* dY, float* db, int batchN, int N, int HW, hipStream_t st) {
+    if (batchN < 0 || N < 0 || HW < 0)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv_bias_grad dims must be >= 0");
+    if (prod(batchN, N, HW) > INT64_C(1) << 40)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv_bias_grad: tensor too large");
+    SEERA_TRY(check_ptrs(N > 0, db, prod(batchN, N, HW) > 0 ? dY : db, db));
+    return conv_bias_grad(dY, db, batchN, N, HW, st);
+}
 
 int conv2d_bwd_impl(const float* Wt, const float* X, const float* dY, float* dX, float* dW,
                     int batch, int C, int H, int W_in, int N, int R, int S, int strideh,
@@ -371,6 +394,36 @@ int seera_hip_conv2d_fwd_async(const float* image, const float* kernel, float* c
     return guarded([&] {
         return queued(conv2d_fwd_impl(image, kernel, conv, batchN, C, H, W, N, R, S, pad_h,
                                       pad_w, stride_h, stride_w, as_stream(stream)));
+    });
+}
+int seera_hip_conv2d_fwd_bias_act(const float* image, const float* kernel, const float* bias,
+                                  float* conv, float* mask, int batchN, int C, int H, int W, int N,
+                                  int R, int S, int pad_h, int pad_w, int stride_h, int stride_w,
+                                  int act) {
+    return guarded([&] {
+        return sync_after(conv2d_fwd_bias_act_impl(image, kernel, bias, conv, mask, batchN, C, H,
+                                                   W, N, R, S, pad_h, pad_w, stride_h, stride_w,
+                                                   act, nullptr));
+    });
+}
+int seera_hip_conv2d_fwd_bias_act_async(const float* image, const float* kernel,
+                                        const float* bias, float* conv, float* mask, int batchN,
+                                        int C, int H, int W, int N, int R, int S, int pad_h,
+                                        int pad_w, int stride_h, int stride_w, int act,
+                                        void* stream) {
+    return guarded([&] {
+        return queued(conv2d_fwd_bias_act_impl(image, kernel, bias, conv, mask, batchN, C, H, W,
+                                               N, R, S, pad_h, pad_w, stride_h, stride_w, act,
+                                               as_stream(stream)));
+    });
+}
+int seera_hip_conv_bias_grad(const float* dY, float* db, int batchN, int N, int HW) {
+    return guarded([&] { return sync_after(conv_bias_grad_impl(dY, db, batchN, N, HW, nullptr)); });
+}
+int seera_hip_conv_bias_grad_async(const float* dY, float* db, int batchN, int N, int HW,
+                                   void* stream) {
+    return guarded([&] {
+        return queued(conv_bias_grad_impl(dY, db, batchN, N, HW, as_stream(stream)));
     });
 }
 int seera_hip_conv2d_fwd(const float* image, const float* kernel, float* conv, int batchN, int C,

@@ -161,6 +161,7 @@ struct PixelProblem {
     int M, N, K;
     int64_t ldc, split_stride;  // unused: this problem is never split
     int tiles_n, k_split, gm;
+    ConvEpi epi;                // forward only: bias [M] and activation
 
     template <int R, int BK, int NT>
     using SA = StageKC<R, BK, NT, VA>;
@@ -181,7 +182,12 @@ struct PixelProblem {
     }
     __device__ __forceinline__ void store(int m, int n, int, float v) const {
         const int b = n / out_hw;
-        C[((int64_t)b * M + m) * out_hw + (n - b * out_hw)] = v;
+        const int64_t i = ((int64_t)b * M + m) * out_hw + (n - b * out_hw);
+        if (epi.bias || epi.act)
+            epilogue(C + i, epi.mask ? epi.mask + i : nullptr, v, epi.bias ? epi.bias[m] : 0.f,
+                     epi.act);
+        else
+            C[i] = v;
     }
 };
 
@@ -233,15 +239,18 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
-int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
-             int S, int sh, int sw, int ph, int pw, hipStream_t st) {
+namespace {
+
+int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F,
+                 int R, int S, int sh, int sw, int ph, int pw, const ConvEpi& epi,
+                 hipStream_t st) {
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
     const int64_t npix = (int64_t)B * Ho * Wo, K = (int64_t)C * R * S;
     if (npix > 0x7fffffff || K > 0x7fffffff || (int64_t)B * C * H * W > (int64_t)1 << 40)
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
     if (npix == 0 || F == 0) return SEERA_OK;
     bool used = false;
-    SEERA_TRY(band_conv_fwd(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used));
+    SEERA_TRY(band_conv_fwd(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi));
     if (used) return SEERA_OK;
     // Gather path: any width, any tile size.
     FwdGather g{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)npix};
@@ -250,10 +259,80 @@ int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int
     auto fill = [&](auto p) {
         p.Wm = Wt; p.ldw = K; p.g = g; p.C = Y; p.out_hw = Ho * Wo;
         p.M = F; p.N = (int)npix; p.K = (int)K; p.ldc = 0; p.split_stride = 0;
+        p.epi = epi;
         return p;
     };
     if (va) return run_plan<true>(fill(PixelProblem<4, FwdGather>{}), pl, st);
     return run_plan<true>(fill(PixelProblem<1, FwdGather>{}), pl, st);
+}
+
+// db[f] = sum over (b, p) of dY[b, f, p], in a fixed order: block (f, g)
+// adds images [g*per, (g+1)*per) -- each thread a strided subset, then a
+// tree over the block -- into part[f, g]; a second kernel adds the G parts
+// of each f in g order.
+constexpr int kCbThreads = 256;
+
+__global__ __launch_bounds__(kCbThreads) void conv_bias_partial(const float* __restrict__ dY,
+                                                                float* __restrict__ part, int B,
+                                                                int F, int HW, int per, int G) {
+    __shared__ float red[kCbThreads];
+    const int f = blockIdx.x / G, g = blockIdx.x % G;
+    const int b0 = g * per, b1 = min(B, b0 + per);
+    float s = 0.f;
+    for (int b = b0; b < b1; ++b) {
+        const float* row = dY + ((int64_t)b * F + f) * HW;
+        for (int p = threadIdx.x; p < HW; p += kCbThreads) s += row[p];
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+#pragma unroll
+    for (int w = kCbThreads / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ void conv_bias_finish(const float* __restrict__ part, float* __restrict__ db, int F,
+                                 int G) {
+    const int f = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= F) return;
+    float t = 0.f;
+    for (int g = 0; g < G; ++g) t += part[(int64_t)f * G + g];
+    db[f] = t;
+}
+
+}  // namespace
+
+int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
+             int S, int sh, int sw, int ph, int pw, hipStream_t st) {
+    return conv_fwd_epi(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, ConvEpi{}, st);
+}
+
+int conv_fwd_bias_act(const float* X, const float* Wt, const float* bias, float* Y, float* mask,
+                      int B, int C, int H, int W, int F, int R, int S, int sh, int sw, int ph,
+                      int pw, int act, hipStream_t st) {
+    return conv_fwd_epi(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, ConvEpi{bias, mask, act},
+                        st);
+}
+
+int conv_bias_grad(const float* dY, float* db, int B, int F, int HW, hipStream_t st) {
+    if (F == 0) return SEERA_OK;
+    if (B == 0 || HW == 0) return fill_f32(db, 0.f, (size_t)F, st);
+    // About 2048 blocks in all, at least one image each.
+    const int G = std::max(1, std::min(B, 2048 / F));
+    const int per = (B + G - 1) / G;
+    const int Gu = (B + per - 1) / per;  // groups that hold an image
+    void* ws = nullptr;
+    SEERA_TRY(workspace(sizeof(float) * (size_t)F * Gu, &ws));
+    float* part = static_cast<float*>(ws);
+    hipLaunchKernelGGL(conv_bias_partial, dim3((unsigned)(F * Gu)), dim3(kCbThreads), 0, st, dY,
+                       part, B, F, HW, per, Gu);
+    SEERA_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(conv_bias_finish, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, st, part,
+                       db, F, Gu);
+    SEERA_HIP_TRY(hipGetLastError());
+    return SEERA_OK;
 }
 
 int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, int Hi, int Wi,

@@ -28,6 +28,17 @@ struct BandPhase {
     int block0;      // first blockIdx.x of the phase
 };
 
+// Fused forward epilogue of a Conv2D layer (Seera.py:254-257: conv2d, then
+// + bias [1, F, 1, 1], then the activation): bias [F] (nullptr: none) added in
+// fp32 to each output of filter f, then act (0 none, 1 ReLU: out = v > 0 ? v
+// : 0, mask = v > 0 ? 1 : 0 when mask [B, F, Hout, Wout] is not nullptr).
+// All zero: a plain convolution.
+struct ConvEpi {
+    const float* bias;
+    float* mask;
+    int act;
+};
+
 struct BandConvArgs {
     const float* in;     // [B, C, H, W] fp32
     const half_t* wk;    // prepared fp16 weights
@@ -42,12 +53,14 @@ struct BandConvArgs {
     int64_t lds_bytes;
     int nphase;
     BandPhase ph[kBandMaxPhases];
+    ConvEpi epi;         // forward only; zero for the transposed launches
 };
 
 // Forward convolution Y = conv(X, W) (W [F, C, R, S]) when the band path
 // applies (input width % 4 == 0, tile fits LDS); *used reports whether it ran.
 int band_conv_fwd(const float* X, const float* W, float* Y, int B, int C, int H, int W_in, int F,
-                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used);
+                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used,
+                  const ConvEpi& epi = {});
 
 // Transposed convolution out[B, Cc, H, W] of Y [B, Fc, Hi, Wi] with the conv
 // weight W [Fc, Cc, R, S] (stride, pad of the forward conv), by stride phases.

@@ -186,7 +186,13 @@ __global__ __launch_bounds__(kNT) void band_conv_kernel(const BandConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int f = fb0 + r;
-                if (f < a.F) a.out[((int64_t)b * a.F + f) * a.Hout * a.Wout + opix] = acc[fi][i][r];
+                if (f >= a.F) continue;
+                const int64_t oi = ((int64_t)b * a.F + f) * a.Hout * a.Wout + opix;
+                if (a.epi.bias || a.epi.act)
+                    epilogue(a.out + oi, a.epi.mask ? a.epi.mask + oi : nullptr, acc[fi][i][r],
+                             a.epi.bias ? a.epi.bias[f] : 0.f, a.epi.act);
+                else
+                    a.out[oi] = acc[fi][i][r];
             }
         }
     }
@@ -436,7 +442,13 @@ __global__ __launch_bounds__(kNT) void band_conv_pipe(const BandConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int f = fb0 + r;
-                if (f < a.F) a.out[((int64_t)b * a.F + f) * a.Hout * a.Wout + opix] = acc[fi][i][r];
+                if (f >= a.F) continue;
+                const int64_t oi = ((int64_t)b * a.F + f) * a.Hout * a.Wout + opix;
+                if (a.epi.bias || a.epi.act)
+                    epilogue(a.out + oi, a.epi.mask ? a.epi.mask + oi : nullptr, acc[fi][i][r],
+                             a.epi.bias ? a.epi.bias[f] : 0.f, a.epi.act);
+                else
+                    a.out[oi] = acc[fi][i][r];
             }
         }
     }
@@ -993,12 +1005,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace
 
 int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F,
-                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used) {
+                  int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used,
+                  const ConvEpi& epi) {
     *used = false;
     if (W % 4 != 0 || !aligned16(X)) return SEERA_OK;
     BandConvArgs a{};
     a.in = X;
     a.out = Y;
+    a.epi = epi;
     a.B = B; a.C = C; a.H = H; a.W = W;
     a.F = F;
     a.Hout = (H + 2 * ph - R) / sh + 1;

@@ -76,6 +76,7 @@ struct StreamArgs {
     int64_t lds_bytes;
     int nphase;
     BandPhase ph[kBandMaxPhases];  // nrb = strips, ncb = column tiles
+    ConvEpi epi;                   // fused bias / activation (zero: none)
 };
 
 // UC: every phase has 3 column taps (0: any).
@@ -198,6 +199,33 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Hout * a.Wout);
         const int hw = a.Hout * a.Wout;
         const int fl = ftile * 64 + (lane & 15);  // filter of this lane (+ fg*16)
+        // Fused epilogue (the bias and ReLU of a Conv2D layer): bias of each of
+        // this lane's 4 filters, and the mask image (written when ReLU asks
+        // for it, at the output's offsets: mask = out > 0, which is v > 0).
+        const bool epi_on = a.epi.bias || a.epi.act;
+        const bool mask_on = a.epi.mask && a.epi.act == kActRelu;
+        float bv[4];
+#pragma unroll
+        for (int fg = 0; fg < 4; ++fg)
+            bv[fg] = a.epi.bias && fl + fg * 16 < a.F ? a.epi.bias[fl + fg * 16] : 0.f;
+        const rsrc_t mask_img =
+            make_rsrc(mask_on ? a.epi.mask + (int64_t)b * a.F * a.Hout * a.Wout : a.out);
+        auto finish = [&](floatx4_t v, int fg) {
+            if (epi_on) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float t = v[j] + bv[fg];
+                    v[j] = a.epi.act == kActRelu ? (t > 0.f ? t : 0.f) : t;
+                }
+            }
+            return v;
+        };
+        auto mask_of = [](floatx4_t v) {
+            floatx4_t m;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m[j] = v[j] > 0.f ? 1.f : 0.f;
+            return m;
+        };
         const int px0 = (wave / kG) * PXG * 16;   // first pixel of this wave's half row
         // Pixel fragment offsets within a ring plane per column tap (UC == 3).
         int poff[UC == 3 ? 3 : 1][PXG];
@@ -216,9 +244,14 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         uint32_t roff[UC == 3 ? PXG : 1][4];
         bool pending = false;
 #define SEERA_STREAM_FLUSH(PG, FG0)                                                         \
-    _Pragma("unroll") for (int fg = (FG0); fg < (FG0) + 2; ++fg)                            \
+    _Pragma("unroll") for (int fg = (FG0); fg < (FG0) + 2; ++fg) {                          \
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, res[PG][fg]),   \
-                                               dst_img, roff[PG][fg], 0, 0);
+                                               dst_img, roff[PG][fg], 0, 0);                \
+        if (mask_on)                                                                        \
+            __builtin_amdgcn_raw_buffer_store_b128(                                         \
+                __builtin_bit_cast(uintx4_t, mask_of(res[PG][fg])), mask_img, roff[PG][fg], \
+                0, 0);                                                                      \
+    }
         for (int s = 0; s < nsteps; ++s) {
             __syncthreads();  // the rows of step s are in the ring
             const int o = s * kG + wave % kG - sh;  // output row of this wave (strip-relative)
@@ -345,11 +378,15 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
                     const uint32_t off =
                         pok && f < a.F ? (uint32_t)((f * hw + orow + ow0 + px) * 4) : kBufOOB;
                     if constexpr (UC == 3) {
-                        res[pg][fg] = acc[pg][fg];
+                        res[pg][fg] = finish(acc[pg][fg], fg);
                         roff[pg][fg] = off;
                     } else {
-                        __builtin_amdgcn_raw_buffer_store_b128(
-                            __builtin_bit_cast(uintx4_t, acc[pg][fg]), dst_img, off, 0, 0);
+                        const floatx4_t v = finish(acc[pg][fg], fg);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, v),
+                                                               dst_img, off, 0, 0);
+                        if (mask_on)
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                __builtin_bit_cast(uintx4_t, mask_of(v)), mask_img, off, 0, 0);
                     }
                 }
             }
@@ -472,7 +509,7 @@ int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     *used = false;
     if (band.ish != 1 || band.isw != 1 || band.nphase < 1) return SEERA_OK;
     StreamArgs a{};
-    a.in = band.in; a.wk = band.wk; a.out = band.out;
+    a.in = band.in; a.wk = band.wk; a.out = band.out; a.epi = band.epi;
     a.B = band.B; a.C = band.C; a.H = band.H; a.W = band.W;
     a.F = band.F; a.Hout = band.Hout; a.Wout = band.Wout;
     a.osh = band.osh; a.osw = band.osw;

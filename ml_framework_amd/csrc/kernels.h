@@ -34,6 +34,13 @@ int fill_f32(float* p, float v, size_t n, hipStream_t st);
 // Y[B, F, Ho, Wo] = conv(X[B, C, H, W], Wt[F, C, R, S]).
 int conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F, int R,
              int S, int sh, int sw, int ph, int pw, hipStream_t st);
+// Y = act(conv(X, Wt) + bias[f]) in the convolution's store; bias [F] or
+// nullptr, act 0 (none) or 1 (ReLU, mask [B, F, Ho, Wo] = Y > 0 if not null).
+int conv_fwd_bias_act(const float* X, const float* Wt, const float* bias, float* Y, float* mask,
+                      int B, int C, int H, int W, int F, int R, int S, int sh, int sw, int ph,
+                      int pw, int act, hipStream_t st);
+// db[F] = sum over images and pixels of dY[B, F, HW], fixed order.
+int conv_bias_grad(const float* dY, float* db, int B, int F, int HW, hipStream_t st);
 // out[B, C, H, W] = transposed conv of Y[B, F, Hi, Wi] with W[F, C, R, S].
 int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, int Hi, int Wi,
                int C, int H, int W, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);

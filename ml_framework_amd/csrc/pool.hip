@@ -23,7 +23,7 @@
 // dout * mask[i], the windows in (ho, wo) order, starting from +0; the
 // reference adds the same terms with atomics, in any order.
 //
-// Two kernel pairs:
+// Kernel pairs:
 //   * cells (stride >= window on both axes, e.g. the usual 2x2 stride 2):
 //     windows do not overlap, so the plane splits into one cell per output --
 //     rows [ho*sh - ph, (ho+1)*sh - ph), the last output row also taking the
@@ -41,8 +41,31 @@
 namespace seera {
 namespace {
 
+// Unsigned 32-bit division by a divisor fixed at launch, as one multiply-high,
+// an add and a shift (Granlund and Montgomery, "Division by Invariant
+// Integers using Multiplication", PLDI 1994, section 4): with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> l for every 32-bit n (the sum taken in 64
+// bits). A generic division costs about 25 VALU instructions per lane, and
+// the pool kernels are otherwise memory-bound.
+struct FastDiv {
+    unsigned d, m, l;
+};
+
+FastDiv make_fastdiv(unsigned d) {
+    unsigned l = 0;
+    while ((1ull << l) < d) ++l;
+    const unsigned m = (unsigned)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    return {d, m, l};
+}
+
+__device__ __forceinline__ unsigned fdiv(unsigned n, FastDiv f) {
+    return (unsigned)(((unsigned long long)__umulhi(n, f.m) + n) >> f.l);
+}
+
 struct PoolGeom {
     int H, W, R, S, ph, pw, sh, sw, Ho, Wo;
+    FastDiv dH, dW, dsh, dsw, dHo, dWo;
 };
 
 // Cell of output index o along one axis: [lo, hi) of the input, clipped.
@@ -58,8 +81,8 @@ __global__ __launch_bounds__(256) void maxpool_fwd_cells(const float* __restrict
                                                          unsigned total) {
     const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const unsigned wo = i % g.Wo, t = i / g.Wo;
-    const unsigned ho = t % g.Ho, bc = t / g.Ho;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
     const unsigned plane = bc * (unsigned)(g.H * g.W);
     const float* xp = x + plane;
     int* mp = mask + plane;
@@ -91,8 +114,8 @@ __global__ __launch_bounds__(256) void maxpool_bwd_cells(const float* __restrict
                                                          unsigned total) {
     const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const unsigned wo = i % g.Wo, t = i / g.Wo;
-    const unsigned ho = t % g.Ho, bc = t / g.Ho;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
     const unsigned plane = bc * (unsigned)(g.H * g.W);
     const int* mp = mask + plane;
     float* dp = dx + plane;
@@ -114,14 +137,63 @@ __global__ __launch_bounds__(256) void maxpool_bwd_cells(const float* __restrict
     }
 }
 
+// The cells kernels for 2x2 windows, stride 2, no padding and an even W
+// (the reference's MaxPool2D default): every cell row is an aligned pair of
+// elements, moved as one 8-byte access. With W even there is no column tail;
+// with H odd the last output row's cell has a third row, all outside windows.
+__global__ __launch_bounds__(256) void maxpool_fwd_2x2(const float* __restrict__ x,
+                                                       float* __restrict__ out,
+                                                       int* __restrict__ mask, PoolGeom g,
+                                                       unsigned total) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
+    const unsigned k0 = bc * (unsigned)(g.H * g.W) + 2 * ho * g.W + 2 * wo;
+    const float2 a = *reinterpret_cast<const float2*>(x + k0);
+    const float2 b = *reinterpret_cast<const float2*>(x + k0 + g.W);
+    // Visit order (0,0) (0,1) (1,0) (1,1); the origin is (0,0), so it starts
+    // as the argmax and each later element >= the max takes over.
+    float best = a.x;
+    int arg = 0;
+    if (best <= a.y) best = a.y, arg = 1;
+    if (best <= b.x) best = b.x, arg = 2;
+    if (best <= b.y) best = b.y, arg = 3;
+    out[i] = best;
+    *reinterpret_cast<int2*>(mask + k0) = make_int2(arg == 0, arg == 1);
+    *reinterpret_cast<int2*>(mask + k0 + g.W) = make_int2(arg == 2, arg == 3);
+    if ((g.H & 1) && ho == (unsigned)g.Ho - 1)
+        *reinterpret_cast<int2*>(mask + k0 + 2 * g.W) = make_int2(0, 0);
+}
+
+__global__ __launch_bounds__(256) void maxpool_bwd_2x2(const float* __restrict__ dout,
+                                                       const int* __restrict__ mask,
+                                                       float* __restrict__ dx, PoolGeom g,
+                                                       unsigned total) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
+    const unsigned k0 = bc * (unsigned)(g.H * g.W) + 2 * ho * g.W + 2 * wo;
+    const float d = dout[i];
+    const int2 m0 = *reinterpret_cast<const int2*>(mask + k0);
+    const int2 m1 = *reinterpret_cast<const int2*>(mask + k0 + g.W);
+    *reinterpret_cast<float2*>(dx + k0) =
+        make_float2(0.f + d * (float)m0.x, 0.f + d * (float)m0.y);
+    *reinterpret_cast<float2*>(dx + k0 + g.W) =
+        make_float2(0.f + d * (float)m1.x, 0.f + d * (float)m1.y);
+    if ((g.H & 1) && ho == (unsigned)g.Ho - 1)
+        *reinterpret_cast<float2*>(dx + k0 + 2 * g.W) = make_float2(0.f, 0.f);
+}
+
 __global__ __launch_bounds__(256) void maxpool_fwd_general(const float* __restrict__ x,
                                                            float* __restrict__ out,
                                                            int* __restrict__ mask, PoolGeom g,
                                                            unsigned total) {
     const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    const unsigned wo = i % g.Wo, t = i / g.Wo;
-    const unsigned ho = t % g.Ho, bc = t / g.Ho;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
     const unsigned plane = bc * (unsigned)(g.H * g.W);
     const float* xp = x + plane;
     const int h0 = (int)ho * g.sh - g.ph, w0 = (int)wo * g.sw - g.pw;
@@ -154,14 +226,17 @@ __global__ __launch_bounds__(256) void maxpool_bwd_general(const float* __restri
     // The reference's terms dout * (float)mask: for a 0 mask they still turn
     // a non-finite dout into NaN.
     const float m = (float)mask[i];
-    const int w = (int)(i % g.W);
-    const unsigned t = i / g.W;
-    const int h = (int)(t % g.H);
-    const unsigned bc = t / g.H;
+    const unsigned t = fdiv(i, g.dW), bc = fdiv(t, g.dH);
+    const int w = (int)(i - t * g.W), h = (int)(t - bc * g.H);
     const float* gp = dout + bc * (unsigned)(g.Ho * g.Wo);
-    auto lo = [](int num, int den) { return num <= 0 ? 0 : (num + den - 1) / den; };
-    const int ho0 = lo(h + g.ph - g.R + 1, g.sh), ho1 = min(g.Ho - 1, (h + g.ph) / g.sh);
-    const int wo0 = lo(w + g.pw - g.S + 1, g.sw), wo1 = min(g.Wo - 1, (w + g.pw) / g.sw);
+    // ceil(num / den) for num > 0, else 0; num + den - 1 < 2^22 here.
+    auto lo = [](int num, int den, FastDiv f) {
+        return num <= 0 ? 0 : (int)fdiv((unsigned)(num + den - 1), f);
+    };
+    const int ho0 = lo(h + g.ph - g.R + 1, g.sh, g.dsh);
+    const int ho1 = min(g.Ho - 1, (int)fdiv((unsigned)(h + g.ph), g.dsh));
+    const int wo0 = lo(w + g.pw - g.S + 1, g.sw, g.dsw);
+    const int wo1 = min(g.Wo - 1, (int)fdiv((unsigned)(w + g.pw), g.dsw));
     float sum = 0.f;
     for (int ho = ho0; ho <= ho1; ++ho)
         for (int wo = wo0; wo <= wo1; ++wo) sum += gp[ho * g.Wo + wo] * m;
@@ -169,10 +244,18 @@ __global__ __launch_bounds__(256) void maxpool_bwd_general(const float* __restri
 }
 
 PoolGeom geom(int H, int W, int R, int S, int ph, int pw, int sh, int sw) {
-    return {H, W, R, S, ph, pw, sh, sw, (H + 2 * ph - R) / sh + 1, (W + 2 * pw - S) / sw + 1};
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    return {H, W, R, S, ph, pw, sh, sw, Ho, Wo,
+            make_fastdiv(H), make_fastdiv(W), make_fastdiv(sh), make_fastdiv(sw),
+            make_fastdiv(Ho), make_fastdiv(Wo)};
 }
 
 unsigned blocks(unsigned n) { return (n + 255u) / 256u; }
+
+bool pair_path(int R, int S, int ph, int pw, int sh, int sw, int W, const void* p0, const void* p1) {
+    return R == 2 && S == 2 && sh == 2 && sw == 2 && ph == 0 && pw == 0 && W % 2 == 0 &&
+           ((uintptr_t)p0 | (uintptr_t)p1) % 8 == 0;
+}
 
 }  // namespace
 
@@ -181,7 +264,10 @@ int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int 
     const PoolGeom g = geom(H, W, R, S, ph, pw, sh, sw);
     const unsigned nin = (unsigned)B * C * H * W, nout = (unsigned)B * C * g.Ho * g.Wo;
     if (nout == 0) return SEERA_OK;
-    if (sh >= R && sw >= S) {
+    if (pair_path(R, S, ph, pw, sh, sw, W, x, mask)) {
+        hipLaunchKernelGGL(maxpool_fwd_2x2, dim3(blocks(nout)), dim3(256), 0, st, x, out, mask,
+                           g, nout);
+    } else if (sh >= R && sw >= S) {
         hipLaunchKernelGGL(maxpool_fwd_cells, dim3(blocks(nout)), dim3(256), 0, st, x, out, mask,
                            g, nout);
     } else {
@@ -198,7 +284,10 @@ int maxpool_bwd(const float* dout, const int* mask, float* dx, int B, int C, int
     const PoolGeom g = geom(H, W, R, S, ph, pw, sh, sw);
     const unsigned nin = (unsigned)B * C * H * W, nout = (unsigned)B * C * g.Ho * g.Wo;
     if (nin == 0) return SEERA_OK;
-    if (sh >= R && sw >= S)
+    if (pair_path(R, S, ph, pw, sh, sw, W, mask, dx))
+        hipLaunchKernelGGL(maxpool_bwd_2x2, dim3(blocks(nout)), dim3(256), 0, st, dout, mask, dx,
+                           g, nout);
+    else if (sh >= R && sw >= S)
         hipLaunchKernelGGL(maxpool_bwd_cells, dim3(blocks(nout)), dim3(256), 0, st, dout, mask,
                            dx, g, nout);
     else

@@ -121,4 +121,6 @@ MAXPOOL = [
     ("q01", 2, 3, 11, 11, 2, 2, 3, 0),
     ("q02", 1, 2, 5, 7, 2, 2, 1, 2),
     ("q03", 2, 3, 13, 10, 3, 3, 2, 1),
+    ("q04", 2, 3, 9, 10, 2, 2, 2, 0),    # 2x2 s2, odd H: a tail row under the last windows
+    ("q05", 2, 3, 8, 9, 2, 2, 2, 0),     # 2x2 s2, odd W: a tail column
 ]

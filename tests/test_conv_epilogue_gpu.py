@@ -1,0 +1,109 @@
+"""Fused Conv2D-layer forward (convolution + bias + ReLU in the conv's store)
+and the conv bias gradient. The reference's Conv2D layer (Seera.py:254-257)
+runs cuda_conv2d_fwd, then + bias [1, F, 1, 1] (broadcast_add_4d,
+broadcast.cu:12-64) and the activation (cuda_relu_fwd, activations.cu:9-15);
+the fused entry point must equal that sequence bit for bit: it is checked
+against the unfused GPU convolution with the fp32 bias add and ReLU done in
+numpy, on shapes that take each forward kernel (row streaming, band, gather).
+db is the reference's sum of dY over axes 3, 2 and 0 (Seera_Engine.py:42-65),
+checked against an fp64 sum."""
+import numpy as np
+import pytest
+
+from ml_framework_amd import capi
+from ml_framework_amd.capi import DeviceBuffer
+from tests.helpers import hip_conv_fwd, out_hw
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _gpu():
+    assert capi.gpu_available(), "no HIP device visible"
+
+
+# (name, N, C, H, W, F, K, stride, pad)
+SHAPES = [
+    ("stream3x3", 4, 64, 56, 56, 64, 3, 1, 1),    # config 4's kernel at batch 4
+    ("stream_2ft", 2, 96, 20, 20, 80, 3, 1, 1),     # 2 filter tiles, 80 filters
+    ("stream5x5", 3, 16, 24, 24, 24, 5, 1, 2),
+    ("band_s2", 8, 32, 64, 64, 64, 3, 2, 1),       # strided: band kernel
+    ("band_2x2s2", 4, 32, 32, 32, 64, 2, 2, 0),    # 4 taps, small band
+    ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),      # width % 4 != 0: gather GEMM
+    ("gather_1f", 4, 8, 9, 9, 1, 3, 1, 1),         # one filter
+]
+
+
+def _fused(x, w, bias, s, p, act, with_mask=True):
+    N, C, H, W = x.shape
+    F, _, KH, KW = w.shape
+    OH, OW = out_hw(H, W, KH, KW, s, p)
+    n_out = N * F * OH * OW
+    with DeviceBuffer.from_array(x) as px, DeviceBuffer.from_array(w) as pw, \
+            DeviceBuffer(n_out * 4) as py, DeviceBuffer(n_out * 4) as pm:
+        pb = DeviceBuffer.from_array(bias) if bias is not None else None
+        pm.fill(0x7F)
+        try:
+            capi.call("seera_hip_conv2d_fwd_bias_act", px.ptr, pw.ptr, pb.ptr if pb else None,
+                      py.ptr, pm.ptr if with_mask else None, N, C, H, W, F, KH, KW, p, p, s, s,
+                      act)
+        finally:
+            if pb:
+                pb.close()
+        return py.to_array((N, F, OH, OW)), pm.to_array((N, F, OH, OW))
+
+
+@pytest.mark.parametrize("case", SHAPES, ids=[c[0] for c in SHAPES])
+@pytest.mark.parametrize("act", [capi.SEERA_ACT_NONE, capi.SEERA_ACT_RELU])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fused_conv_equals_unfused(case, act, with_bias):
+    _, N, C, H, W, F, K, s, p = case
+    r = np.random.default_rng(N * 100 + C + F + K)
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (r.standard_normal((F, C, K, K)) * 0.2).astype(np.float32)
+    bias = r.uniform(-0.5, 0.5, F).astype(np.float32) if with_bias else None
+    y = hip_conv_fwd(x, w, s, p)
+    z = y + (bias[None, :, None, None] if with_bias else np.float32(0))
+    want = np.where(z > 0, z, np.float32(0)) if act == capi.SEERA_ACT_RELU else z
+    got, mask = _fused(x, w, bias, s, p, act)
+    assert np.array_equal(got, want)
+    if act == capi.SEERA_ACT_RELU:
+        assert np.array_equal(mask, (z > 0).astype(np.float32))
+        assert 0.2 < mask.mean() < 0.8
+
+
+def test_mask_optional_and_activation_checked():
+    r = np.random.default_rng(3)
+    x = r.standard_normal((2, 16, 12, 12)).astype(np.float32)
+    w = r.standard_normal((8, 16, 3, 3)).astype(np.float32)
+    b = r.standard_normal(8).astype(np.float32)
+    got, _ = _fused(x, w, b, 1, 1, capi.SEERA_ACT_RELU, with_mask=False)
+    z = hip_conv_fwd(x, w, 1, 1) + b[None, :, None, None]
+    assert np.array_equal(got, np.where(z > 0, z, np.float32(0)))
+    lib = capi.load()
+    st = lib.seera_hip_conv2d_fwd_bias_act(None, None, None, None, None, 1, 1, 4, 4, 1, 3, 3,
+                                           1, 1, 1, 1, 7)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and b"activation" in lib.seera_hip_last_error()
+
+
+@pytest.mark.parametrize("N,F,H,W", [(128, 64, 56, 56), (32, 64, 56, 56), (3, 5, 7, 9),
+                                     (1, 1, 1, 1), (4000, 3, 2, 2), (2, 300, 4, 4)])
+def test_conv_bias_grad(N, F, H, W):
+    dy = np.random.default_rng(N + F).standard_normal((N, F, H, W)).astype(np.float32)
+    with DeviceBuffer.from_array(dy) as pd, DeviceBuffer(F * 4) as pb:
+        capi.call("seera_hip_conv_bias_grad", pd.ptr, pb.ptr, N, F, H * W)
+        db = pb.to_array((F,))
+    ref = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    bound = 1e-6 * np.abs(dy).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-6
+    assert np.all(np.abs(db - ref) <= bound), float(np.max(np.abs(db - ref) / bound))
+    # Fixed order: a second call gives the same bits.
+    with DeviceBuffer.from_array(dy) as pd, DeviceBuffer(F * 4) as pb:
+        capi.call("seera_hip_conv_bias_grad", pd.ptr, pb.ptr, N, F, H * W)
+        assert np.array_equal(pb.to_array((F,)), db)
+
+
+def test_conv_bias_grad_empty_batch_is_zero():
+    with DeviceBuffer(16) as pb:
+        pb.fill(0x7F)
+        capi.call("seera_hip_conv_bias_grad", None, pb.ptr, 0, 4, 9)
+        assert np.array_equal(pb.to_array((4,)), np.zeros(4, np.float32))

@@ -144,3 +144,26 @@ def test_async_entry_points_on_a_stream():
                 assert np.array_equal(pd.to_array(x.shape), dx)
     finally:
         lib.seera_hip_stream_destroy(st.value)
+
+
+def test_unaligned_pointers_match_aligned():
+    """2x2 stride 2 moves element pairs as 8-byte accesses when x, mask and dX
+    are 8-byte aligned; 4-byte-aligned pointers take the element-wise kernels
+    and give the same bits."""
+    x = np.random.default_rng(11).standard_normal((2, 3, 10, 12)).astype(np.float32)
+    out, mask = hip_maxpool(x, 2, 2, 0, 2)
+    dout = np.random.default_rng(12).standard_normal(out.shape).astype(np.float32)
+    dx = hip_maxpool_bwd(dout, mask, 2, 2, 0, 2)
+    N, C, H, W = x.shape
+    n = x.size
+    with DeviceBuffer(4 * n + 4) as px, DeviceBuffer(out.nbytes) as po, \
+            DeviceBuffer(4 * n + 4) as pm, DeviceBuffer.from_array(dout) as pg, \
+            DeviceBuffer(4 * n + 4) as pd:
+        capi.check(capi.load().seera_hip_memcpy_h2d(px.ptr + 4, x.ctypes.data, x.nbytes))
+        args = (N, C, H, W, 2, 2, 0, 0, 2, 2)
+        capi.call("seera_hip_maxpool_fwd", px.ptr + 4, po.ptr, pm.ptr + 4, *args)
+        capi.call("seera_hip_maxpool_bwd", pg.ptr, pm.ptr + 4, pd.ptr + 4, *args)
+        got_m = pm.to_array((n + 1,), np.int32)[1:].reshape(x.shape)
+        got_dx = pd.to_array((n + 1,))[1:].reshape(x.shape)
+        assert np.array_equal(po.to_array(out.shape), out)
+        assert np.array_equal(got_m, mask) and np.array_equal(got_dx, dx)
