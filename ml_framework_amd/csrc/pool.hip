@@ -215,6 +215,89 @@ __global__ __launch_bounds__(256) void maxpool_fwd_general(const float* __restri
     if (arg >= 0) mask[plane + (unsigned)arg] = 1;
 }
 
+// The general kernels with the window (forward) or the covering-window count
+// per axis (backward) fixed at compile time: every load of a thread is issued
+// before the first is used. The loop kernels wait for each load in turn,
+// which left them bound by memory latency.
+template <int RR, int SS>
+__global__ __launch_bounds__(256) void maxpool_fwd_general_t(const float* __restrict__ x,
+                                                             float* __restrict__ out,
+                                                             int* __restrict__ mask, PoolGeom g,
+                                                             unsigned total) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const unsigned t = fdiv(i, g.dWo), wo = i - t * g.Wo;
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
+    const unsigned plane = bc * (unsigned)(g.H * g.W);
+    const float* xp = x + plane;
+    const int h0 = (int)ho * g.sh - g.ph, w0 = (int)wo * g.sw - g.pw;
+    float v[RR][SS];
+    bool ok[RR][SS];
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+        for (int s = 0; s < SS; ++s) {
+            const int h = h0 + r, w = w0 + s;
+            ok[r][s] = h >= 0 && h < g.H && w >= 0 && w < g.W;
+            v[r][s] = ok[r][s] ? xp[h * g.W + w] : 0.f;
+        }
+    float best = ok[0][0] ? v[0][0] : 0.f;  // the origin, or 0 in the padding
+    int arg = -1;
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+        for (int s = 0; s < SS; ++s)
+            if (ok[r][s] && best <= v[r][s]) {
+                best = v[r][s];
+                arg = (h0 + r) * g.W + w0 + s;
+            }
+    out[i] = best;
+    if (arg >= 0) mask[plane + (unsigned)arg] = 1;
+}
+
+// MH, MW: the most windows that cover one element along each axis,
+// ceil(R / sh) and ceil(S / sw). Candidate windows outside the covering range
+// add +0, which leaves the (ho, wo)-ordered sum unchanged (it starts at +0 and
+// never becomes -0 under round-to-nearest). Each wave takes 64 columns of one
+// input row (grid x: groups of 4 rows of all planes, grid y: 64-column
+// tiles), so the row's plane, covering output rows and dout row are
+// wave-uniform and only the column arithmetic is per lane.
+template <int MH, int MW>
+__global__ __launch_bounds__(256) void maxpool_bwd_general_t(const float* __restrict__ dout,
+                                                             const int* __restrict__ mask,
+                                                             float* __restrict__ dx, PoolGeom g,
+                                                             unsigned nrows) {
+    const unsigned row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int w = (int)(blockIdx.y * 64 + (threadIdx.x & 63));
+    if (row >= nrows || w >= g.W) return;
+    const unsigned bc = fdiv(row, g.dH);
+    const int h = (int)(row - bc * g.H);
+    const unsigned i = row * (unsigned)g.W + (unsigned)w;
+    const float m = (float)mask[i];
+    const float* gp = dout + bc * (unsigned)(g.Ho * g.Wo);
+    auto lo = [](int num, int den, FastDiv f) {
+        return num <= 0 ? 0 : (int)fdiv((unsigned)(num + den - 1), f);
+    };
+    const int ho0 = lo(h + g.ph - g.R + 1, g.sh, g.dsh);
+    const int ho1 = min(g.Ho - 1, (int)fdiv((unsigned)(h + g.ph), g.dsh));
+    const int wo0 = lo(w + g.pw - g.S + 1, g.sw, g.dsw);
+    const int wo1 = min(g.Wo - 1, (int)fdiv((unsigned)(w + g.pw), g.dsw));
+    float term[MH][MW];
+#pragma unroll
+    for (int a = 0; a < MH; ++a)
+#pragma unroll
+        for (int c = 0; c < MW; ++c) {
+            const int ho = ho1 - (MH - 1) + a, wo = wo1 - (MW - 1) + c;
+            term[a][c] = ho >= ho0 && wo >= wo0 ? gp[ho * g.Wo + wo] * m : 0.f;
+        }
+    float sum = 0.f;
+#pragma unroll
+    for (int a = 0; a < MH; ++a)
+#pragma unroll
+        for (int c = 0; c < MW; ++c) sum += term[a][c];
+    dx[i] = sum;
+}
+
 // One thread per input element: the windows covering row h are
 // ho in [ceil((h + ph - R + 1) / sh), floor((h + ph) / sh)] within [0, Ho).
 __global__ __launch_bounds__(256) void maxpool_bwd_general(const float* __restrict__ dout,
@@ -252,6 +335,36 @@ PoolGeom geom(int H, int W, int R, int S, int ph, int pw, int sh, int sw) {
 
 unsigned blocks(unsigned n) { return (n + 255u) / 256u; }
 
+template <int MH, int MW>
+void launch_bwd_t(const float* dout, const int* mask, float* dx, const PoolGeom& g, unsigned n,
+                  hipStream_t st) {
+    const unsigned nrows = n / (unsigned)g.W;  // B * C * H
+    hipLaunchKernelGGL((maxpool_bwd_general_t<MH, MW>),
+                       dim3((nrows + 3) / 4, (unsigned)((g.W + 63) / 64)), dim3(256), 0, st, dout,
+                       mask, dx, g, nrows);
+}
+
+template <int MH>
+void launch_bwd_mw(int mw, const float* dout, const int* mask, float* dx, const PoolGeom& g,
+                   unsigned n, hipStream_t st) {
+    if (mw == 1) launch_bwd_t<MH, 1>(dout, mask, dx, g, n, st);
+    else if (mw == 2) launch_bwd_t<MH, 2>(dout, mask, dx, g, n, st);
+    else launch_bwd_t<MH, 3>(dout, mask, dx, g, n, st);
+}
+
+int launch_bwd_general(const float* dout, const int* mask, float* dx, const PoolGeom& g,
+                       unsigned n, hipStream_t st) {
+    const int mh = (g.R + g.sh - 1) / g.sh, mw = (g.S + g.sw - 1) / g.sw;
+    if (mh > 3 || mw > 3)
+        hipLaunchKernelGGL(maxpool_bwd_general, dim3(blocks(n)), dim3(256), 0, st, dout, mask,
+                           dx, g, n);
+    else if (mh == 1) launch_bwd_mw<1>(mw, dout, mask, dx, g, n, st);
+    else if (mh == 2) launch_bwd_mw<2>(mw, dout, mask, dx, g, n, st);
+    else launch_bwd_mw<3>(mw, dout, mask, dx, g, n, st);
+    SEERA_HIP_TRY(hipGetLastError());
+    return SEERA_OK;
+}
+
 bool pair_path(int R, int S, int ph, int pw, int sh, int sw, int W, const void* p0, const void* p1) {
     return R == 2 && S == 2 && sh == 2 && sw == 2 && ph == 0 && pw == 0 && W % 2 == 0 &&
            ((uintptr_t)p0 | (uintptr_t)p1) % 8 == 0;
@@ -272,8 +385,15 @@ int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int 
                            g, nout);
     } else {
         SEERA_HIP_TRY(hipMemsetAsync(mask, 0, sizeof(int) * (size_t)nin, st));
-        hipLaunchKernelGGL(maxpool_fwd_general, dim3(blocks(nout)), dim3(256), 0, st, x, out,
-                           mask, g, nout);
+        if (R == 2 && S == 2)
+            hipLaunchKernelGGL((maxpool_fwd_general_t<2, 2>), dim3(blocks(nout)), dim3(256), 0,
+                               st, x, out, mask, g, nout);
+        else if (R == 3 && S == 3)
+            hipLaunchKernelGGL((maxpool_fwd_general_t<3, 3>), dim3(blocks(nout)), dim3(256), 0,
+                               st, x, out, mask, g, nout);
+        else
+            hipLaunchKernelGGL(maxpool_fwd_general, dim3(blocks(nout)), dim3(256), 0, st, x, out,
+                               mask, g, nout);
     }
     SEERA_HIP_TRY(hipGetLastError());
     return SEERA_OK;
@@ -291,8 +411,7 @@ int maxpool_bwd(const float* dout, const int* mask, float* dx, int B, int C, int
         hipLaunchKernelGGL(maxpool_bwd_cells, dim3(blocks(nout)), dim3(256), 0, st, dout, mask,
                            dx, g, nout);
     else
-        hipLaunchKernelGGL(maxpool_bwd_general, dim3(blocks(nin)), dim3(256), 0, st, dout, mask,
-                           dx, g, nin);
+        SEERA_TRY(launch_bwd_general(dout, mask, dx, g, nin, st));
     SEERA_HIP_TRY(hipGetLastError());
     return SEERA_OK;
 }

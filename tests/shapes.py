@@ -123,4 +123,5 @@ MAXPOOL = [
     ("q03", 2, 3, 13, 10, 3, 3, 2, 1),
     ("q04", 2, 3, 9, 10, 2, 2, 2, 0),    # 2x2 s2, odd H: a tail row under the last windows
     ("q05", 2, 3, 8, 9, 2, 2, 2, 0),     # 2x2 s2, odd W: a tail column
+    ("q06", 2, 3, 10, 11, 4, 4, 1, 1),   # 4 windows cover an element per axis: loop kernels
 ]
