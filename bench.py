@@ -375,6 +375,10 @@ def main():
             "ms_fwd": round(cv["ms_fwd"], 4), "ms_bwd": round(cv["ms_bwd"], 4),
             "ms_fwd_fused_bias_relu": round(cv["ms_fwd_fused_bias_relu"], 4),
             "ms_bias_grad": round(cv["ms_bias_grad"], 4),
+            # Algorithmic HBM bytes: fwd reads X, writes Y (2 x 102.8 MB); bwd's
+            # dX pass reads dY, writes dX and its dW pass reads X and dY (4 x).
+            "fwd_hbm_frac": round(2 * 102.76e6 / (cv["ms_fwd"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "bwd_hbm_frac": round(4 * 102.76e6 / (cv["ms_bwd"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
             "fwd_bwd_tflops": round(conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3) / 1e12, 2),
             "pct_mfma_peak": round(100 * conv_flops / ((cv["ms_fwd"] + cv["ms_bwd"]) * 1e-3)
                                    / 1e12 / PEAK_FP16_TFLOPS, 2),

@@ -272,6 +272,9 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
 // of each f in g order.
 constexpr int kCbThreads = 256;
 
+// VEC: HW % 4 == 0 and dY 16-byte aligned; each thread adds float4s, the
+// four lanes of one in sequence.
+template <bool VEC>
 __global__ __launch_bounds__(kCbThreads) void conv_bias_partial(const float* __restrict__ dY,
                                                                 float* __restrict__ part, int B,
                                                                 int F, int HW, int per, int G) {
@@ -281,7 +284,18 @@ __global__ __launch_bounds__(kCbThreads) void conv_bias_partial(const float* __r
     float s = 0.f;
     for (int b = b0; b < b1; ++b) {
         const float* row = dY + ((int64_t)b * F + f) * HW;
-        for (int p = threadIdx.x; p < HW; p += kCbThreads) s += row[p];
+        if constexpr (VEC) {
+            const float4* row4 = reinterpret_cast<const float4*>(row);
+            for (int p = threadIdx.x; p < HW / 4; p += kCbThreads) {
+                const float4 v = row4[p];
+                s += v.x;
+                s += v.y;
+                s += v.z;
+                s += v.w;
+            }
+        } else {
+            for (int p = threadIdx.x; p < HW; p += kCbThreads) s += row[p];
+        }
     }
     red[threadIdx.x] = s;
     __syncthreads();
@@ -326,8 +340,12 @@ int conv_bias_grad(const float* dY, float* db, int B, int F, int HW, hipStream_t
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(float) * (size_t)F * Gu, &ws));
     float* part = static_cast<float*>(ws);
-    hipLaunchKernelGGL(conv_bias_partial, dim3((unsigned)(F * Gu)), dim3(kCbThreads), 0, st, dY,
-                       part, B, F, HW, per, Gu);
+    if (HW % 4 == 0 && aligned16(dY))
+        hipLaunchKernelGGL(conv_bias_partial<true>, dim3((unsigned)(F * Gu)), dim3(kCbThreads), 0,
+                           st, dY, part, B, F, HW, per, Gu);
+    else
+        hipLaunchKernelGGL(conv_bias_partial<false>, dim3((unsigned)(F * Gu)), dim3(kCbThreads), 0,
+                           st, dY, part, B, F, HW, per, Gu);
     SEERA_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(conv_bias_finish, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, st, part,
                        db, F, Gu);
