@@ -403,7 +403,7 @@ int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, i
     p.split_stride = 0;
     if (npix == 0) {
         // Empty contraction: dW = 0.
-        SEERA_HIP_TRY(hipMemsetAsync(dW, 0, sizeof(float) * (size_t)F * crs, st));
+        SEERA_TRY(fill_f32(dW, 0.f, (size_t)F * crs, st));  // a kernel: safe under graph capture
         return SEERA_OK;
     }
     bool used = false;

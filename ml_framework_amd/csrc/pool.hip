@@ -384,7 +384,9 @@ int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int 
         hipLaunchKernelGGL(maxpool_fwd_cells, dim3(blocks(nout)), dim3(256), 0, st, x, out, mask,
                            g, nout);
     } else {
-        SEERA_HIP_TRY(hipMemsetAsync(mask, 0, sizeof(int) * (size_t)nin, st));
+        // Clear with a kernel (all-zero bits are int 0), not a memset node,
+        // so that the call can be captured into a graph.
+        SEERA_TRY(fill_f32(reinterpret_cast<float*>(mask), 0.f, (size_t)nin, st));
         if (R == 2 && S == 2)
             hipLaunchKernelGGL((maxpool_fwd_general_t<2, 2>), dim3(blocks(nout)), dim3(256), 0,
                                st, x, out, mask, g, nout);
