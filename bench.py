@@ -251,10 +251,21 @@ def bench_mlp(steps, warmup, stream):
     ms_plain = timed(fwd_plain, steps, warmup, stream)
     ms_fused = timed(fwd_fused, steps, warmup, stream)
     ms_db = timed(bias_grads, steps, warmup, stream)
+    # The same step captured once into a HIP graph and replayed: one launch per
+    # step instead of one per kernel (the step is launch-bound at this size).
+    import ctypes
+
+    capi.check(lib.seera_hip_graph_capture_begin(stream.ptr))
+    step()
+    g = ctypes.c_void_p()
+    capi.check(lib.seera_hip_graph_capture_end(stream.ptr, ctypes.byref(g)))
+    ms_graph = timed(lambda: capi.check(lib.seera_hip_graph_launch(g.value, stream.ptr)), steps,
+                     warmup, stream)
+    capi.check(lib.seera_hip_graph_destroy(g.value))
     for v in acts + ws + grads + dws + biases + masks + dbs:
         v.close()
     flops = sum(2 * 256 * i * o * 3 for i, o in zip(dims[:-1], dims[1:]))
-    return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+    return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12, "ms_step_graph": ms_graph,
             "ms_fwd_gemms": ms_plain, "ms_fwd_fused_bias_relu": ms_fused, "ms_bias_grads": ms_db}
 
 

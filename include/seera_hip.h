@@ -243,6 +243,20 @@ int seera_hip_stream_create(void **stream);
 int seera_hip_stream_destroy(void *stream);
 int seera_hip_stream_synchronize(void *stream);
 
+/* HIP graphs of the _async entry points (no counterpart in the reference,
+ * which launches every kernel from Python and synchronizes after each). Begin
+ * capture on a created stream, queue _async calls on it, end capture to get
+ * an executable graph, then replay it with seera_hip_graph_launch: one launch
+ * for the whole sequence, with the pointers and sizes captured. Make one
+ * eager call of each captured call (same sizes) first, so that the library's
+ * workspace is already large enough: growing it allocates, which capture
+ * does not allow. The _async entry points clear memory with kernels, not
+ * memset nodes. */
+int seera_hip_graph_capture_begin(void *stream);
+int seera_hip_graph_capture_end(void *stream, void **graph_exec);
+int seera_hip_graph_launch(void *graph_exec, void *stream);
+int seera_hip_graph_destroy(void *graph_exec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -528,6 +528,40 @@ int seera_hip_stream_destroy(void* stream) {
         return (int)SEERA_OK;
     });
 }
+int seera_hip_graph_capture_begin(void* stream) {
+    return guarded([&] {
+        if (!stream) return fail(SEERA_ERR_INVALID_ARGUMENT, "capture needs a created stream");
+        SEERA_HIP_TRY(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+        return (int)SEERA_OK;
+    });
+}
+int seera_hip_graph_capture_end(void* stream, void** graph_exec) {
+    return guarded([&] {
+        if (!stream || !graph_exec) return fail(SEERA_ERR_INVALID_ARGUMENT, "null argument");
+        *graph_exec = nullptr;
+        hipGraph_t graph = nullptr;
+        SEERA_HIP_TRY(hipStreamEndCapture(as_stream(stream), &graph));
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+        *graph_exec = exec;
+        return (int)SEERA_OK;
+    });
+}
+int seera_hip_graph_launch(void* graph_exec, void* stream) {
+    return guarded([&] {
+        if (!graph_exec) return fail(SEERA_ERR_INVALID_ARGUMENT, "null graph");
+        SEERA_HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+        return queued(SEERA_OK);
+    });
+}
+int seera_hip_graph_destroy(void* graph_exec) {
+    return guarded([&] {
+        if (graph_exec) SEERA_HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+        return (int)SEERA_OK;
+    });
+}
 int seera_hip_stream_synchronize(void* stream) {
     return guarded([&] {
         SEERA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
