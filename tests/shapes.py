@@ -56,6 +56,21 @@ CONV2D_STREAM = [
     ("s10", 2, 8, 6, 16, 8, 1, 3, 1, 1),       # 1x3, one chunk, 1 pixel group
 ]
 
+# Edge shapes (not from the reference's tests): 1x1 image and kernel, channel
+# counts off the 8/32/64 grid, a tall narrow and a wide image (several column
+# tiles), stride 3 with padding 2, a kernel wider than tall, padding larger
+# than half the kernel.
+CONV2D_EDGE = [
+    ("e01", 1, 1, 1, 1, 1, 1, 1, 1, 0),
+    ("e02", 2, 300, 5, 5, 7, 3, 3, 1, 1),
+    ("e03", 1, 8, 200, 3, 4, 3, 3, 1, 1),
+    ("e04", 3, 16, 7, 130, 16, 3, 3, 1, 1),
+    ("e05", 2, 5, 17, 19, 3, 3, 3, 3, 2),
+    ("e06", 2, 24, 12, 16, 40, 1, 7, 1, 0),
+    ("e07", 2, 8, 6, 6, 8, 3, 3, 1, 2),
+    ("e08", 1, 65, 9, 9, 129, 3, 3, 2, 1),
+]
+
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
 CONVT = [
     ("t01", 2, 4, 4, 4, 8, 3, 3, 1, 0),

@@ -12,7 +12,7 @@ from ml_framework_amd import capi
 from oracle import fp16r
 from tests.helpers import (assert_parity, hip_conv_bwd, hip_conv_fwd, hip_convT_bwd,
                            hip_convT_fwd, rel_fro)
-from tests.shapes import CONV2D, CONV2D_STREAM, CONVT
+from tests.shapes import CONV2D, CONV2D_EDGE, CONV2D_STREAM, CONVT
 
 pytestmark = pytest.mark.gpu
 S = oracle.seera_cpp
@@ -29,7 +29,10 @@ def _kaiming(r, shape, fan_in):
     return r.uniform(-lim, lim, shape).astype(np.float32)
 
 
-@pytest.mark.parametrize("case", CONV2D + CONV2D_STREAM, ids=[c[0] for c in CONV2D + CONV2D_STREAM])
+ALL_CONV2D = CONV2D + CONV2D_STREAM + CONV2D_EDGE
+
+
+@pytest.mark.parametrize("case", ALL_CONV2D, ids=[c[0] for c in ALL_CONV2D])
 def test_conv2d_parity(case):
     name, N, C, H, W, F, KH, KW, s, p = case
     r = np.random.default_rng(zlib.crc32(name.encode()))

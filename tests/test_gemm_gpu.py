@@ -222,3 +222,20 @@ def test_mlp_config3_fwd_bwd():
         assert_parity(da, rda, f"dA layer {li}")
         assert_parity(dw, rdw, f"dW layer {li}")
         g = da * (acts[li] > 0)
+
+
+@pytest.mark.parametrize("M,K,N,nb", [(5, 65536, 7, 1), (3, 40, 5, 4000), (1, 4096, 1, 1),
+                                      (300, 1, 200, 1), (2, 3000, 3000, 1), (3000, 8, 2, 3)])
+def test_extreme_aspect_ratios(M, K, N, nb):
+    """Long contractions with tiny outputs (split-K), many tiny batches (dB
+    contracts over Nbatch*M = 12000), K = 1, and skinny panels."""
+    r = np.random.default_rng(M + 7 * K + 13 * N + nb)
+    a = fp16r(r.uniform(-1, 1, (nb, M, K)))
+    b = fp16r(r.uniform(-1, 1, (K, N)))
+    dc = fp16r(r.uniform(-1, 1, (nb, M, N)))
+    got = hip_matmul(a, b)
+    assert_parity(got, S.matmul_batched(a, b), f"C {M}x{K}x{N}x{nb}")
+    da, db = hip_matmul_bwd(a, b, dc)
+    rda, rdb = S.matmul_bwd(a, b, dc)
+    assert_parity(da, rda, "dA")
+    assert_parity(db, rdb, "dB")

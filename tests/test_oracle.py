@@ -20,7 +20,7 @@ import pytest
 import oracle
 from oracle import closed_form as cf
 from oracle import fp16r
-from tests.shapes import CONV2D, CONVT, MATMUL
+from tests.shapes import CONV2D, CONV2D_EDGE, CONVT, MATMUL
 
 S = oracle.seera_cpp
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "demo_matmul.json")
@@ -88,7 +88,7 @@ def test_oracle_gemm_matches_closed_form(M, K, N, nb):
     assert _close(da, da2) and _close(db, db2)
 
 
-@pytest.mark.parametrize("case", CONV2D, ids=[c[0] for c in CONV2D])
+@pytest.mark.parametrize("case", CONV2D + CONV2D_EDGE, ids=[c[0] for c in CONV2D + CONV2D_EDGE])
 def test_oracle_conv2d_matches_closed_form(case):
     name, N, C, H, W, F, KH, KW, s, p = case
     r = _rng(zlib.crc32(name.encode()))
