@@ -269,6 +269,76 @@ def bench_mlp(steps, warmup, stream):
             "ms_fwd_gemms": ms_plain, "ms_fwd_fused_bias_relu": ms_fused, "ms_bias_grads": ms_db}
 
 
+def bench_alloc(reps=50):
+    """The allocation path as the reference drives it: cuTen allocates every
+    op's output with cudaMalloc and frees it afterwards (cuTen.py:77-84), and
+    each binding synchronizes. Timed on the host: one malloc + free of 512 KB
+    from the cache against one that reaches hipMalloc / hipFree (cache emptied
+    first), and the MLP cfg3 step through the synchronous entry points with
+    every output allocated and freed per step, cached against uncached."""
+    import ctypes
+
+    lib = capi.load()
+
+    def pair():
+        p = ctypes.c_void_p()
+        capi.check(lib.seera_hip_malloc(ctypes.byref(p), 512 * 1024))
+        capi.check(lib.seera_hip_free(p.value))
+
+    def per_call_us(fn, n, uncached):
+        # uncached: the cache is emptied before each call (so every malloc
+        # reaches hipMalloc) and after it, inside the timed region (so every
+        # free reaches hipFree), as cudaMalloc / cudaFree per op do.
+        capi.check(lib.seera_hip_synchronize())
+        t = 0.0
+        for _ in range(n):
+            if uncached:
+                capi.check(lib.seera_hip_empty_cache())
+            t0 = time.perf_counter()
+            fn()
+            if uncached:
+                capi.check(lib.seera_hip_empty_cache())
+            t += time.perf_counter() - t0
+        return t / n * 1e6
+
+    pair()
+    cached_us, uncached_us = per_call_us(pair, 10 * reps, False), per_call_us(pair, reps, True)
+    r = np.random.default_rng(0)
+    dims, B = [784, 512, 256, 10], 256
+    x = DeviceBuffer.from_array(fp16r(r.uniform(0, 1, (B, 784))))
+    ws = [DeviceBuffer.from_array(fp16r(r.uniform(-0.05, 0.05, (i, o))))
+          for i, o in zip(dims[:-1], dims[1:])]
+    g_out = DeviceBuffer.from_array(r.standard_normal((B, 10)).astype(np.float32))
+
+    def step():
+        acts = [x]
+        for li in range(3):
+            y = DeviceBuffer(B * dims[li + 1] * 4)
+            capi.call("seera_hip_matmul", acts[li].ptr, ws[li].ptr, y.ptr, B, dims[li + 1],
+                      dims[li], 1)
+            acts.append(y)
+        g = g_out
+        tmp = []
+        for li in (2, 1, 0):
+            da, dw = DeviceBuffer(B * dims[li] * 4), DeviceBuffer(dims[li] * dims[li + 1] * 4)
+            capi.call("seera_hip_matmul_bwd", acts[li].ptr, ws[li].ptr, g.ptr, da.ptr, dw.ptr, B,
+                      dims[li + 1], dims[li], 1)
+            tmp += [da, dw]
+            g = da
+        for v in acts[1:] + tmp:
+            v.close()
+
+    step()
+    ms_cached = per_call_us(step, reps, False) / 1e3
+    ms_uncached = per_call_us(step, reps, True) / 1e3
+    for v in ws + [x, g_out]:
+        v.close()
+    return {"malloc_free_512k_us_cached": round(cached_us, 2),
+            "malloc_free_512k_us_uncached": round(uncached_us, 2),
+            "mlp_step_sync_alloc_ms_cached": round(ms_cached, 4),
+            "mlp_step_sync_alloc_ms_uncached": round(ms_uncached, 4)}
+
+
 def cpu_baseline(n=4096, reps=5):
     """The oracle's seera_cpp restatement (OpenBLAS sgemm) on this host."""
     import oracle
@@ -401,6 +471,7 @@ def main():
             "fwd_bwd_tflops": round(ct_flops / ((ct["ms_fwd"] + ct["ms_bwd"]) * 1e-3) / 1e12, 2),
         }
         extras["mlp_cfg3"] = {k: round(v, 4) for k, v in bench_mlp(20, 3, stream).items()}
+        extras["alloc_path"] = bench_alloc()
         extras["maxpool_2x2_s2"] = bench_maxpool(20, 3, stream, 2, 2, 0)
         extras["maxpool_3x3_s2_p1"] = bench_maxpool(20, 3, stream, 3, 2, 1)
         out["extras"] = extras
