@@ -85,6 +85,22 @@ int seera_hip_matmul_bwd_async(const float *A, const float *B, const float *dC,
                                float *dA, float *dB, int M, int N, int K,
                                int Nbatch, void *stream);
 
+/* No single counterpart in the reference: the backward of a Dense layer whose
+ * input A came out of a ReLU. The reference runs cuda_matmul_bwd, then the
+ * ReLU's chain rule on dA -- local_grad * cp with local_grad the ReLU's 0/1
+ * grad buffer (Seera_Engine.py:575-583; activations.cu:9-15). Here
+ * dA = (dC . B^T) * mask is applied in the dA GEMM's store (mask
+ * [Nbatch*M, K], as written by seera_hip_matmul_bias_act with ReLU, read
+ * only); dB = A^T . dC as in seera_hip_matmul_bwd. Bit-identical to the two
+ * calls. */
+int seera_hip_matmul_bwd_relu(const float *A, const float *B, const float *dC,
+                              const float *mask, float *dA, float *dB, int M,
+                              int N, int K, int Nbatch);
+int seera_hip_matmul_bwd_relu_async(const float *A, const float *B,
+                                    const float *dC, const float *mask,
+                                    float *dA, float *dB, int M, int N, int K,
+                                    int Nbatch, void *stream);
+
 /* No single counterpart in the reference: the Dense-layer forward it runs as
  * three calls -- cuda_matmul (GEMM.cu:95-103), broadcast_add_4d of the bias
  * (broadcast.cu:12-64, 140-146) and cuda_relu_fwd (activations.cu:9-15) --

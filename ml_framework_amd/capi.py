@@ -51,6 +51,8 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_bias_grad_async": ([_vp, _vp, _i, _i, _vp], _i),
     "seera_hip_matmul_bwd": ([_vp] * 5 + [_i] * 4, _i),
     "seera_hip_matmul_bwd_async": ([_vp] * 5 + [_i] * 4 + [_vp], _i),
+    "seera_hip_matmul_bwd_relu": ([_vp] * 6 + [_i] * 4, _i),
+    "seera_hip_matmul_bwd_relu_async": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "seera_hip_transpose_2d": ([_vp, _vp, _i, _i], _i),
     "seera_hip_transpose_3d": ([_vp, _vp, _i, _i, _i], _i),
     "seera_hip_conv2d_fwd": (_conv14, _i),

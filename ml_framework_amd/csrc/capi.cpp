@@ -117,6 +117,15 @@ int matmul_bwd_impl(const float* A, const float* B, const float* dC, float* dA, 
         SEERA_TRY(check_ptrs(true, A, B, dC, dA, dB));
     return gemm_bwd(A, B, dC, dA, dB, M, N, K, Nbatch, st);
 }
+int matmul_bwd_relu_impl(const float* A, const float* B, const float* dC, const float* mask,
+                         float* dA, float* dB, int M, int N, int K, int Nbatch, hipStream_t st) {
+    if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "matmul_bwd dims must be >= 0");
+    if (prod(M, N, K, Nbatch) > 0 || prod(K, N) > 0)
+        SEERA_TRY(check_ptrs(true, A, B, dC, dA, dB));
+    if (prod(M, K, Nbatch) > 0) SEERA_TRY(check_ptrs(true, mask, mask, mask));
+    return gemm_bwd_relu(A, B, dC, mask, dA, dB, M, N, K, Nbatch, st);
+}
 
 int conv2d_fwd_impl(const float* image, const float* kernel, float* conv, int batchN, int C, int H,
                     int W, int N, int R, int S, int pad_h, int pad_w, int stride_h, int stride_w,
@@ -307,6 +316,20 @@ int seera_hip_matmul(const float* A, const float* B, float* C, int M, int N, int
     return guarded([&] { return sync_after(matmul_impl(A, B, C, M, N, K, Nbatch, nullptr)); });
 }
 
+int seera_hip_matmul_bwd_relu(const float* A, const float* B, const float* dC, const float* mask,
+                              float* dA, float* dB, int M, int N, int K, int Nbatch) {
+    return guarded([&] {
+        return sync_after(matmul_bwd_relu_impl(A, B, dC, mask, dA, dB, M, N, K, Nbatch, nullptr));
+    });
+}
+int seera_hip_matmul_bwd_relu_async(const float* A, const float* B, const float* dC,
+                                    const float* mask, float* dA, float* dB, int M, int N, int K,
+                                    int Nbatch, void* stream) {
+    return guarded([&] {
+        return queued(
+            matmul_bwd_relu_impl(A, B, dC, mask, dA, dB, M, N, K, Nbatch, as_stream(stream)));
+    });
+}
 int seera_hip_matmul_bwd_async(const float* A, const float* B, const float* dC, float* dA,
                                float* dB, int M, int N, int K, int Nbatch, void* stream) {
     return guarded(

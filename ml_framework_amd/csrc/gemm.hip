@@ -195,6 +195,17 @@ int gemm_fwd_bias_act(const float* A, const float* B, const float* bias, float* 
     return gemm_dispatch<true, false, true>(A, K, B, N, C, N, (int)Mb, N, K, st, e);
 }
 
+int gemm_bwd_relu(const float* A, const float* B, const float* dC, const float* mask, float* dA,
+                  float* dB, int M, int N, int K, int Nbatch, hipStream_t st) {
+    const int64_t Mb = (int64_t)M * Nbatch;
+    if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    Epi e;
+    e.mask = const_cast<float*>(mask);  // read, not written, under kActReluGrad
+    e.act = kActReluGrad;
+    SEERA_TRY((gemm_dispatch<true, true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st, e)));
+    return gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st);
+}
+
 // db[n] = sum over rows of dY[row, n]: fixed-order partial sums of the rows a
 // thread group owns, added in group order (bit-reproducible run to run).
 constexpr int kBgCols = 64, kBgGroups = 8;

@@ -18,6 +18,9 @@ int bias_grad(const float* dY, float* db, int rows, int N, hipStream_t st);
 // dA = dC . B^T, dB = A^T . dC over the folded batch.
 int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M, int N,
              int K, int Nbatch, hipStream_t st);
+// gemm_bwd with dA = (dC . B^T) * mask (the ReLU backward of A's layer).
+int gemm_bwd_relu(const float* A, const float* B, const float* dC, const float* mask, float* dA,
+                  float* dB, int M, int N, int K, int Nbatch, hipStream_t st);
 // out[b, c, r] = in[b, r, c] for b < batch.
 int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st);
 

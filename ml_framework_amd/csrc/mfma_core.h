@@ -326,8 +326,16 @@ struct WsStageMNC {
 // engine_cuda/src/broadcast.cu:12-64, activations.cu:9-15): the bias is added
 // in fp32 to the fp32 result, and ReLU writes out = v > 0 ? v : 0 and
 // mask = v > 0 ? 1 : 0, so the result is the unfused sequence's, bit for bit.
-constexpr int kActNone = 0, kActRelu = 1;
+//
+// kActReluGrad is the backward of that ReLU fused into the dA GEMM's store:
+// out = v * mask with mask the forward's 0/1 buffer (an input here), the
+// reference's local_grad * cp (Seera_Engine.py:579); no bias is added.
+constexpr int kActNone = 0, kActRelu = 1, kActReluGrad = 2;
 __device__ __forceinline__ void epilogue(float* out, float* mask, float v, float bias, int act) {
+    if (act == kActReluGrad) {
+        *out = v * *mask;
+        return;
+    }
     v += bias;
     if (act == kActRelu) {
         const bool pos = v > 0.f;

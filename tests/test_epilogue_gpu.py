@@ -100,3 +100,41 @@ def test_bias_grad(rows, N):
         ref = dy.astype(np.float64).sum(axis=0)
         # fp32 sums of up to rows/8 terms per group: the error grows with rows
         assert_parity(g1, ref, "db", rel=1e-5, mabs=max(1e-4, rows * 1e-7))
+
+
+BWD_SHAPES = [
+    (256, 784, 512, 1),    # MLP cfg3 layer 1 (dA is [256, 784])
+    (256, 512, 256, 1),
+    (64, 64, 4096, 1),     # long contraction over N: split-K, mask in the reduce
+    (33, 65, 17, 2),       # odd dims, folded batch
+    (2048, 2048, 2048, 1),  # 256x256 warp-specialised tiles
+    (5, 0, 7, 1),          # K = 0: empty dA and dB
+]
+
+
+@pytest.mark.parametrize("M,K,N,nb", BWD_SHAPES)
+def test_fused_relu_backward_equals_unfused(M, K, N, nb):
+    """dA = (dC . B^T) * mask against matmul_bwd followed by the multiply in
+    numpy (fp32, exact for a 0/1 mask); dB unchanged."""
+    r = np.random.default_rng(M + K + N)
+    a = np.maximum(r.standard_normal((nb, M, K)), 0).astype(np.float32)
+    b = r.standard_normal((K, N)).astype(np.float32)
+    dc = r.standard_normal((nb, M, N)).astype(np.float32)
+    mask = (r.uniform(0, 1, (nb, M, K)) > 0.4).astype(np.float32)
+    n_a, n_b = max(a.size, 1), max(b.size, 1)
+    with DeviceBuffer.from_array(a if a.size else np.zeros(1, np.float32)) as pa, \
+            DeviceBuffer.from_array(b if b.size else np.zeros(1, np.float32)) as pb, \
+            DeviceBuffer.from_array(dc) as pdc, \
+            DeviceBuffer.from_array(mask if mask.size else np.zeros(1, np.float32)) as pm, \
+            DeviceBuffer(n_a * 4) as pda, DeviceBuffer(n_b * 4) as pdb, \
+            DeviceBuffer(n_a * 4) as pda2, DeviceBuffer(n_b * 4) as pdb2:
+        capi.call("seera_hip_matmul_bwd", pa.ptr, pb.ptr, pdc.ptr, pda.ptr, pdb.ptr, M, N, K, nb)
+        capi.call("seera_hip_matmul_bwd_relu", pa.ptr, pb.ptr, pdc.ptr, pm.ptr, pda2.ptr, pdb2.ptr,
+                  M, N, K, nb)
+        if a.size == 0:
+            return
+        da = pda.to_array(a.shape)
+        want = da * mask
+        got = pda2.to_array(a.shape)
+        assert np.array_equal(_bits(got), _bits(want))
+        assert np.array_equal(pdb2.to_array(b.shape), pdb.to_array(b.shape))
