@@ -131,6 +131,46 @@ PYBIND11_MODULE(seera_cuda, m) {
                                           stride_h, stride_w));
           },
           "MaxPool2D backward (GPU ptrs)");
+    // Not in the reference: the fused layer entry points of the C ABI (bias,
+    // ReLU and its mask in the GEMM / convolution store; the ReLU backward in
+    // the dA store; fixed-order bias gradients). Pointers as above; mask and
+    // bias may be 0 (none). act: 0 none, 1 ReLU.
+    m.def("cuda_matmul_bias_act",
+          [](uintptr_t A, uintptr_t B, uintptr_t bias, uintptr_t C, uintptr_t mask, int M, int N,
+             int K, int Nbatch, int act) {
+              check(seera_hip_matmul_bias_act(dev<const float>(A), dev<const float>(B),
+                                              dev<const float>(bias), dev<float>(C),
+                                              dev<float>(mask), M, N, K, Nbatch, act));
+          },
+          "C = act(A @ B + bias); ReLU mask into mask (GPU ptrs)");
+    m.def("cuda_matmul_bwd_relu",
+          [](uintptr_t A, uintptr_t B, uintptr_t dC, uintptr_t mask, uintptr_t dA, uintptr_t dB,
+             int M, int N, int K, int Nbatch) {
+              check(seera_hip_matmul_bwd_relu(dev<const float>(A), dev<const float>(B),
+                                              dev<const float>(dC), dev<const float>(mask),
+                                              dev<float>(dA), dev<float>(dB), M, N, K, Nbatch));
+          },
+          "dA = (dC @ B^T) * mask, dB = A^T @ dC (GPU ptrs)");
+    m.def("cuda_bias_grad",
+          [](uintptr_t dY, uintptr_t db, int rows, int N) {
+              check(seera_hip_bias_grad(dev<const float>(dY), dev<float>(db), rows, N));
+          },
+          "db[n] = sum over rows of dY[rows, N] (GPU ptrs)");
+    m.def("cuda_conv2d_fwd_bias_act",
+          [](uintptr_t image, uintptr_t kernel, uintptr_t bias, uintptr_t conv, uintptr_t mask,
+             int batchN, int C, int H, int W, int N, int R, int S, int pad_h, int pad_w,
+             int stride_h, int stride_w, int act) {
+              check(seera_hip_conv2d_fwd_bias_act(
+                  dev<const float>(image), dev<const float>(kernel), dev<const float>(bias),
+                  dev<float>(conv), dev<float>(mask), batchN, C, H, W, N, R, S, pad_h, pad_w,
+                  stride_h, stride_w, act));
+          },
+          "conv = act(conv2d(image, kernel) + bias[n]) (GPU ptrs, pad before stride)");
+    m.def("cuda_conv_bias_grad",
+          [](uintptr_t dY, uintptr_t db, int batchN, int N, int HW) {
+              check(seera_hip_conv_bias_grad(dev<const float>(dY), dev<float>(db), batchN, N, HW));
+          },
+          "db[n] = sum over images and pixels of dY[batchN, N, HW] (GPU ptrs)");
     // Not in the reference: the caching allocator behind cuda_malloc / cuda_free.
     m.def("cuda_empty_cache", []() { check(seera_hip_empty_cache()); },
           "Return the allocator's cached blocks to HIP");

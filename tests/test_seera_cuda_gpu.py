@@ -137,3 +137,46 @@ def test_maxpool_call_sequence(sc):
     assert np.array_equal(sc.to_host_f32(pdx, x.shape), pool.maxpool_bwd(dout, rm, K, K, p, p, s, s))
     for q in (px, pout, pmask, pg, pdx):
         sc.cuda_free(q)
+
+
+def test_fused_layer_entry_points(sc):
+    """The module's fused Dense / Conv2D entry points equal the reference's
+    call sequences (matmul + bias + relu; conv + bias + relu; the ReLU
+    chain rule on dA) bit for bit, and the bias gradients match fp64 sums."""
+    r = np.random.default_rng(8)
+    a = r.standard_normal((64, 48)).astype(np.float32)
+    b = r.standard_normal((48, 32)).astype(np.float32)
+    bias = r.standard_normal(32).astype(np.float32)
+    pa, pb, pbias = sc.to_device_f32(a), sc.to_device_f32(b), sc.to_device_f32(bias)
+    pc, pm, pz = (sc.cuda_malloc_f32(64 * 32) for _ in range(3))
+    sc.cuda_matmul(pa, pb, pz, 64, 32, 48, 1)
+    sc.cuda_matmul_bias_act(pa, pb, pbias, pc, pm, 64, 32, 48, 1, 1)
+    z = sc.to_host_f32(pz, (64, 32)) + bias
+    assert np.array_equal(sc.to_host_f32(pc, (64, 32)), np.where(z > 0, z, np.float32(0)))
+    assert np.array_equal(sc.to_host_f32(pm, (64, 32)), (z > 0).astype(np.float32))
+    dc = r.standard_normal((64, 32)).astype(np.float32)
+    mask_a = (r.uniform(0, 1, (64, 48)) > 0.5).astype(np.float32)
+    pdc, pma = sc.to_device_f32(dc), sc.to_device_f32(mask_a)
+    pda, pdb, pda2, pdb2 = (sc.cuda_malloc_f32(n) for n in (64 * 48, 48 * 32, 64 * 48, 48 * 32))
+    sc.cuda_matmul_bwd(pa, pb, pdc, pda, pdb, 64, 32, 48, 1)
+    sc.cuda_matmul_bwd_relu(pa, pb, pdc, pma, pda2, pdb2, 64, 32, 48, 1)
+    assert np.array_equal(sc.to_host_f32(pda2, (64, 48)), sc.to_host_f32(pda, (64, 48)) * mask_a)
+    pdbias = sc.cuda_malloc_f32(32)
+    sc.cuda_bias_grad(pdc, pdbias, 64, 32)
+    assert np.allclose(sc.to_host_f32(pdbias, (32,)), dc.astype(np.float64).sum(0), atol=1e-4)
+    x = r.standard_normal((2, 8, 10, 12)).astype(np.float32)
+    w = (r.standard_normal((16, 8, 3, 3)) * 0.2).astype(np.float32)
+    cb = r.standard_normal(16).astype(np.float32)
+    px, pw, pcb = sc.to_device_f32(x), sc.to_device_f32(w), sc.to_device_f32(cb)
+    py, py2, pym = (sc.cuda_malloc_f32(2 * 16 * 10 * 12) for _ in range(3))
+    sc.cuda_conv2d_fwd(px, pw, py, 2, 8, 10, 12, 16, 3, 3, 1, 1, 1, 1)
+    sc.cuda_conv2d_fwd_bias_act(px, pw, pcb, py2, pym, 2, 8, 10, 12, 16, 3, 3, 1, 1, 1, 1, 1)
+    zc = sc.to_host_f32(py, (2, 16, 10, 12)) + cb[None, :, None, None]
+    assert np.array_equal(sc.to_host_f32(py2, (2, 16, 10, 12)), np.where(zc > 0, zc, np.float32(0)))
+    pcdb = sc.cuda_malloc_f32(16)
+    sc.cuda_conv_bias_grad(py2, pcdb, 2, 16, 120)
+    ref = sc.to_host_f32(py2, (2, 16, 10, 12)).astype(np.float64).sum((0, 2, 3))
+    assert np.allclose(sc.to_host_f32(pcdb, (16,)), ref, rtol=1e-5, atol=1e-4)
+    for q in (pa, pb, pbias, pc, pm, pz, pdc, pma, pda, pdb, pda2, pdb2, pdbias, px, pw, pcb, py,
+              py2, pym, pcdb):
+        sc.cuda_free(q)
