@@ -292,6 +292,32 @@ def bench_mlp(steps, warmup, stream):
             "ms_bwd_gemms": ms_bwd_plain, "ms_bwd_fused_relu_grad": ms_bwd_fused}
 
 
+def bench_transpose(steps, warmup, stream):
+    """cuda_transpose_2d / _3d (GEMM.cu:108-150) at 4096 x 4096 and a batch of
+    16 x 1024 x 1024: a bit copy, 8 algorithmic bytes per element."""
+    import ctypes
+
+    lib = capi.load()
+    t = lib.seera_hip_transpose_2d
+    n = 4096
+    src, dst = DeviceBuffer(n * n * 4), DeviceBuffer(n * n * 4)
+    src.fill(0x3F)
+    # The synchronous entry points are the reference's; time them on the null
+    # stream with events (each call ends with a device synchronize).
+    null = Stream.__new__(Stream)
+    null.ptr = None
+    ms2 = timed(lambda: capi.check(t(src.ptr, dst.ptr, n, n)), steps, warmup, null)
+    ms3 = timed(lambda: capi.check(lib.seera_hip_transpose_3d(src.ptr, dst.ptr, 16, 1024, 1024)),
+                steps, warmup, null)
+    src.close()
+    dst.close()
+    nbytes = 8 * n * n
+    # Per call, including the device synchronize each call ends with.
+    return {"ms_2d_4096_per_call": round(ms2, 5), "ms_3d_16x1024_per_call": round(ms3, 5),
+            "gbs_2d_per_call": round(nbytes / (ms2 * 1e-3) / 1e9, 1),
+            "gbs_3d_per_call": round(nbytes / (ms3 * 1e-3) / 1e9, 1)}
+
+
 def bench_alloc(reps=50):
     """The allocation path as the reference drives it: cuTen allocates every
     op's output with cudaMalloc and frees it afterwards (cuTen.py:77-84), and
@@ -494,6 +520,7 @@ def main():
             "fwd_bwd_tflops": round(ct_flops / ((ct["ms_fwd"] + ct["ms_bwd"]) * 1e-3) / 1e12, 2),
         }
         extras["mlp_cfg3"] = {k: round(v, 4) for k, v in bench_mlp(20, 3, stream).items()}
+        extras["transpose"] = bench_transpose(20, 3, stream)
         extras["alloc_path"] = bench_alloc()
         extras["maxpool_2x2_s2"] = bench_maxpool(20, 3, stream, 2, 2, 0)
         extras["maxpool_3x3_s2_p1"] = bench_maxpool(20, 3, stream, 3, 2, 1)
