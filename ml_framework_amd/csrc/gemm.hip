@@ -174,6 +174,37 @@ __global__ __launch_bounds__(256) void transpose_tiles(const float* __restrict__
     }
 }
 
+// The same with 16-byte accesses when rows and cols are multiples of 4 and
+// both tensors 16-byte aligned: a thread reads 4 consecutive columns of one
+// input row and writes 4 consecutive columns (input rows) of one output row.
+__global__ __launch_bounds__(256) void transpose_tiles4(const float* __restrict__ in,
+                                                        float* __restrict__ out, int rows,
+                                                        int cols) {
+    __shared__ float t[64][65];
+    const int64_t slice = (int64_t)rows * cols;
+    in += blockIdx.z * slice;
+    out += blockIdx.z * slice;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int q = threadIdx.x & 15, ty = threadIdx.x >> 4;  // quad column, row group
+    for (int i = ty; i < 64; i += 16) {
+        const int r = r0 + i, c = c0 + 4 * q;
+        if (r < rows && c < cols) {  // c < cols means all 4 (cols % 4 == 0)
+            const float4 v = *reinterpret_cast<const float4*>(in + (int64_t)r * cols + c);
+            t[i][4 * q] = v.x;
+            t[i][4 * q + 1] = v.y;
+            t[i][4 * q + 2] = v.z;
+            t[i][4 * q + 3] = v.w;
+        }
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 16) {
+        const int c = c0 + i, r = r0 + 4 * q;
+        if (c < cols && r < rows)
+            *reinterpret_cast<float4*>(out + (int64_t)c * rows + r) =
+                make_float4(t[4 * q][i], t[4 * q + 1][i], t[4 * q + 2][i], t[4 * q + 3][i]);
+    }
+}
+
 }  // namespace
 
 int gemm_fwd(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch,
@@ -253,7 +284,10 @@ int transpose(const float* in, float* out, int batch, int rows, int cols, hipStr
     dim3 grid((cols + 63) / 64, (rows + 63) / 64, batch);
     if (grid.y > 65535 || grid.z > 65535)
         return fail(SEERA_ERR_INVALID_ARGUMENT, "transpose extent too large");
-    hipLaunchKernelGGL(transpose_tiles, grid, dim3(256), 0, st, in, out, rows, cols);
+    if (rows % 4 == 0 && cols % 4 == 0 && aligned16(in) && aligned16(out))
+        hipLaunchKernelGGL(transpose_tiles4, grid, dim3(256), 0, st, in, out, rows, cols);
+    else
+        hipLaunchKernelGGL(transpose_tiles, grid, dim3(256), 0, st, in, out, rows, cols);
     SEERA_HIP_TRY(hipGetLastError());
     return SEERA_OK;
 }

@@ -164,7 +164,8 @@ def test_square_8192_sampled_rows():
     assert_parity(db[:, cols], a.T.astype(np.float64) @ dc[:, cols], "dB cols")
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (64, 64), (65, 127), (1000, 3), (513, 2049)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (64, 64), (65, 127), (1000, 3), (513, 2049),
+                                       (4, 8), (1000, 12), (256, 4100), (4096, 4096)])
 def test_transpose_2d_bit_exact(rows, cols):
     a = np.random.default_rng(rows + cols).standard_normal((rows, cols)).astype(np.float32)
     with DeviceBuffer.from_array(a) as pi, DeviceBuffer(a.nbytes) as po:
@@ -172,7 +173,7 @@ def test_transpose_2d_bit_exact(rows, cols):
         assert np.array_equal(po.to_array((cols, rows)), a.T)
 
 
-@pytest.mark.parametrize("nb,M,K", [(1, 7, 9), (3, 64, 65), (5, 130, 33)])
+@pytest.mark.parametrize("nb,M,K", [(1, 7, 9), (3, 64, 65), (5, 130, 33), (2, 128, 260), (3, 68, 4)])
 def test_transpose_3d_bit_exact(nb, M, K):
     a = np.random.default_rng(M * K).standard_normal((nb, M, K)).astype(np.float32)
     with DeviceBuffer.from_array(a) as pi, DeviceBuffer(a.nbytes) as po:
