@@ -155,3 +155,24 @@ def test_validation_maxpool(args, what):
     for name in ("seera_hip_maxpool_fwd", "seera_hip_maxpool_bwd"):
         st, msg = _status(name, 1, 1, 1, *args)
         assert st == capi.SEERA_ERR_INVALID_ARGUMENT and what in msg, (name, msg)
+
+
+def test_validation_fused_entry_points():
+    """Argument checks of the entry points with no reference counterpart run
+    before any device work."""
+    st, msg = _status("seera_hip_conv2d_fwd_bias_act", 1, 1, None, 1, None, 1, 1, 4, 4, 1, 3, 3,
+                      1, 1, 1, 1, 5)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "activation" in msg, msg
+    st, msg = _status("seera_hip_conv2d_fwd_bias_act", 1, 1, None, 1, None, 1, 1, 2, 4, 1, 5, 3,
+                      0, 1, 1, 1, 1)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "larger" in msg, msg
+    st, msg = _status("seera_hip_conv_bias_grad", 1, 1, -1, 4, 9)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "dims" in msg, msg
+    st, msg = _status("seera_hip_matmul_bwd_relu", 1, 1, 1, None, 1, 1, 4, 4, 4, 1)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "null" in msg, msg
+    st, msg = _status("seera_hip_matmul_bias_act", 1, 1, None, 1, None, 4, 4, 4, 1, 3)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "activation" in msg, msg
+    st, msg = _status("seera_hip_graph_capture_begin", None)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT, msg
+    st, msg = _status("seera_hip_graph_launch", None, None)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT, msg
