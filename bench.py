@@ -499,6 +499,14 @@ def main():
     }
     if not args.no_extras:
         extras = {"gemm_fwd_bwd_4096_tflops": round(3 * flops / (g["ms_fwd_bwd"] * 1e-3) / 1e12, 2)}
+        # The rest of config 2's sweep (forward and forward+backward).
+        sweep = {}
+        for m in (1024, 2048, 8192):
+            gm = bench_gemm(m, 20 if m < 8192 else 8, 3, stream, True)
+            f = 2.0 * m ** 3
+            sweep[str(m)] = {"fwd_tflops": round(f / (gm["ms_fwd"] * 1e-3) / 1e12, 2),
+                             "fwd_bwd_tflops": round(3 * f / (gm["ms_fwd_bwd"] * 1e-3) / 1e12, 2)}
+        extras["gemm_sweep_cfg2"] = sweep
         cv = bench_conv(20, 3, stream)
         conv_flops = 29.6e9 * 3  # 2*N*F*Ho*Wo*C*R*S per pass, 3 passes
         extras["conv2d_cfg4"] = {
