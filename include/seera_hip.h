@@ -247,6 +247,119 @@ int seera_hip_conv2DTranspose_bwd_async(const float *W, const float *X,
                                         int stridew, int padh, int padw,
                                         void *stream);
 
+/* ---- the functions around the path: activations, softmax, element-wise,
+ * scalar, broadcast, unpooling and reductions. cuTen.py and Seera_Engine.py
+ * call them on every layer (bias add cuTen.py:160, activation cuTen.py:329,
+ * softmax head cuTen.py:401, bias gradient cuTen.py:490). All are
+ * synchronous: the result is ready on return. Sizes are element counts.
+ * Exact fp32 in the reference's order except where noted: the transcendental
+ * functions (exp, log, tanh, pow) come from the device math library and the
+ * softmax sums run in a fixed butterfly order. ---- */
+
+/* Activations: out = f(x) and grad = f'(x), the local gradient the autograd
+ * multiplies in later (activations.cu:9-85, 164-198; bindings
+ * cuda_bindings.cpp:176-239):
+ *   relu    out = x > 0 ? x : 0,         grad = x > 0 ? 1 : 0
+ *   sigmoid out = s = 1/(1 + exp(-x)),   grad = s (1 - s)
+ *   tanh    out = t = tanh(x),           grad = 1 - t t
+ *   log     out = log(x),                grad = 1 / x
+ *   exp     out = e = exp(x),            grad = e
+ *   abs     out = |x|,                   grad = sign(x) (0 at 0)
+ *   sqrt    out = s = sqrt(x),           grad = 0.5 / (s + 1e-12)
+ *   pow     out = x^p,                   grad = p x^(p-1)
+ *   clip    out = min(max(x, lo), hi),   grad = lo <= x <= hi ? 1 : 0 */
+int seera_hip_relu_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_sigmoid_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_tanh_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_log_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_exp_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_abs_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_sqrt_fwd(const float *x, float *out, float *grad, int size);
+int seera_hip_pow_fwd(const float *x, float exponent, float *out, float *grad,
+                      int size);
+int seera_hip_clip_fwd(const float *x, float lo, float hi, float *out,
+                       float *grad, int size);
+
+/* cuda_softmax_fwd (activations.cu:87-127, 201-204; binding
+ * cuda_bindings.cpp:243-247): out[n] = exp(x[n] - max) / sum over each row
+ * of x [N, C]. */
+int seera_hip_softmax_fwd(const float *x, float *out, int N, int C);
+/* cuda_softmax_vjp (activations.cu:129-161, 206-209; binding
+ * cuda_bindings.cpp:249-253): dx = s * (dout - <s, dout>) per row, with s
+ * the softmax output. */
+int seera_hip_softmax_vjp(const float *s, const float *dout, float *dx, int N,
+                          int C);
+
+/* cuda_unpooling_fwd (unpooling.cu:7-26, 55-76; binding cuda_bindings.cpp:
+ * 358-363): out [batchN, C, H*sh, W*sw], out[.., h, w] = inp[.., h/sh, w/sw]. */
+int seera_hip_unpooling_fwd(const float *inp, float *out, int batchN, int C,
+                            int H, int W, int sh, int sw);
+/* cuda_unpooling_bwd (unpooling.cu:28-50, 78-98; binding cuda_bindings.cpp:
+ * 365-370): dx [batchN, C, H, W] = sum of dout over each sh x sw block, row
+ * by row. */
+int seera_hip_unpooling_bwd(const float *dout, float *dx, int batchN, int C,
+                            int H, int W, int sh, int sw);
+
+/* Reductions along axis `dim` of a row-major tensor whose ndims extents are
+ * in the HOST array dimarr (reductionKernels.cu:12-207; bindings
+ * cuda_bindings.cpp:376-421). out holds the product of the other extents:
+ *   sum   in index order from +0;   mean = that sum / extent
+ *   max / min   fmax / fmin from the first element
+ *   argmax / argmin   index (int32) of the last element >= / <= all before */
+int seera_hip_sum_fwd(const float *A, float *out, int ndims, int dim,
+                      const int *dimarr);
+int seera_hip_mean_fwd(const float *A, float *out, int ndims, int dim,
+                       const int *dimarr);
+int seera_hip_max_fwd(const float *A, float *out, int ndims, int dim,
+                      const int *dimarr);
+int seera_hip_min_fwd(const float *A, float *out, int ndims, int dim,
+                      const int *dimarr);
+int seera_hip_argmax_fwd(const float *A, int *out, int ndims, int dim,
+                         const int *dimarr);
+int seera_hip_argmin_fwd(const float *A, int *out, int ndims, int dim,
+                         const int *dimarr);
+/* Their backward (reductionKernels.cu:209-380; bindings cuda_bindings.cpp:
+ * 426-457), dA with the forward input's shape, every element written:
+ *   sum / mean   dA = dOut (/ extent for mean) along the axis
+ *   max / min    dA = dOut at the first element equal to the forward output
+ *                fwdOutput, 0 elsewhere */
+int seera_hip_sum_bwd(const float *dOut, float *dA, int ndims, int dim,
+                      const int *dimarr);
+int seera_hip_mean_bwd(const float *dOut, float *dA, int ndims, int dim,
+                       const int *dimarr);
+int seera_hip_max_bwd(const float *dOut, const float *fwdInput,
+                      const float *fwdOutput, float *dA, int ndims, int dim,
+                      const int *dimarr);
+int seera_hip_min_bwd(const float *dOut, const float *fwdInput,
+                      const float *fwdOutput, float *dA, int ndims, int dim,
+                      const int *dimarr);
+
+/* In place: arr *= k, arr += k, arr = pow(arr, k) (cuTen_essentails.cu:44-51,
+ * 17-24, 53-60, wrappers 88-146; bindings cuda_bindings.cpp:461-465, 479-481). */
+int seera_hip_scaler_multiply_f(float *arr, float k, int total_elements);
+int seera_hip_scaler_add_f(float *arr, float k, int total_elements);
+int seera_hip_power_of(float *arr, float k, int total_elements);
+
+/* C = A op B element by element (elemops.cu:14-40, 46-81; bindings
+ * cuda_bindings.cpp:486-512). */
+int seera_hip_elemadd(const float *A, const float *B, float *C, int size);
+int seera_hip_elemsub(const float *A, const float *B, float *C, int size);
+int seera_hip_elemdiv(const float *A, const float *B, float *C, int size);
+int seera_hip_elemmult(const float *A, const float *B, float *C, int size);
+
+/* 4-D broadcast (broadcast.cu:12-153; bindings cuda_bindings.cpp:518-532):
+ * C = A + B or A * B, where each axis of C has the extent of A or B that is
+ * not 1 and an operand's extent-1 axes are read at index 0; C must hold the
+ * broadcast shape. Shapes that do not broadcast fail with
+ * SEERA_ERR_INVALID_ARGUMENT (the reference prints a message and writes
+ * nothing). */
+int seera_hip_broadcast_add_4d(const float *A, const float *B, float *C,
+                               int aN, int aC, int aH, int aW, int bN, int bC,
+                               int bH, int bW);
+int seera_hip_broadcast_mul_4d(const float *A, const float *B, float *C,
+                               int aN, int aC, int aH, int aW, int bN, int bC,
+                               int bH, int bW);
+
 /* ---- timing (no reference counterpart; used by bench.py) ---- */
 
 /* Events on `stream`: create / record / elapsed milliseconds / destroy. */
@@ -263,15 +376,29 @@ int seera_hip_stream_synchronize(void *stream);
  * which launches every kernel from Python and synchronizes after each). Begin
  * capture on a created stream, queue _async calls on it, end capture to get
  * an executable graph, then replay it with seera_hip_graph_launch: one launch
- * for the whole sequence, with the pointers and sizes captured. Make one
- * eager call of each captured call (same sizes) first, so that the library's
- * workspace is already large enough: growing it allocates, which capture
- * does not allow. The _async entry points clear memory with kernels, not
- * memset nodes. */
+ * for the whole sequence, with the pointers and sizes captured.
+ *
+ * Workspace rule. Temporaries (split-K partials, re-laid-out weights, dW
+ * partials) live in a library workspace, one per (device, stream): _async
+ * calls on two streams never share one. A graph keeps the workspace address
+ * of its capture stream, so:
+ *   - make one eager call of each captured call (same sizes, same stream)
+ *     before capturing; a call that would have to grow the workspace during
+ *     capture fails with SEERA_ERR_INVALID_ARGUMENT;
+ *   - while a graph is live on a device, a workspace that grows keeps its old
+ *     buffer (replays keep writing there) until the device's last graph is
+ *     destroyed, so eager calls of any size may run between replays;
+ *   - a replay and an eager call queued on the capture stream itself are
+ *     ordered; a replay on another stream must not overlap eager calls on the
+ *     capture stream (they share that stream's workspace).
+ * The _async entry points clear memory with kernels, not memset nodes. */
 int seera_hip_graph_capture_begin(void *stream);
 int seera_hip_graph_capture_end(void *stream, void **graph_exec);
 int seera_hip_graph_launch(void *graph_exec, void *stream);
 int seera_hip_graph_destroy(void *graph_exec);
+/* Bytes held by the library's workspaces (all devices and streams) and the
+ * number of old workspace buffers kept alive for live graphs. */
+int seera_hip_workspace_stats(size_t *held_bytes, size_t *retired_buffers);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,27 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_graph_capture_end": ([_vp, ctypes.POINTER(_vp)], _i),
     "seera_hip_graph_launch": ([_vp, _vp], _i),
     "seera_hip_graph_destroy": ([_vp], _i),
+    "seera_hip_workspace_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
+    # activations, softmax, unpooling, reductions, scalar, element-wise, broadcast
+    **{f"seera_hip_{n}_fwd": ([_vp, _vp, _vp, _i], _i)
+       for n in ("relu", "sigmoid", "tanh", "log", "exp", "abs", "sqrt")},
+    "seera_hip_pow_fwd": ([_vp, _f, _vp, _vp, _i], _i),
+    "seera_hip_clip_fwd": ([_vp, _f, _f, _vp, _vp, _i], _i),
+    "seera_hip_softmax_fwd": ([_vp, _vp, _i, _i], _i),
+    "seera_hip_softmax_vjp": ([_vp, _vp, _vp, _i, _i], _i),
+    "seera_hip_unpooling_fwd": ([_vp, _vp] + [_i] * 6, _i),
+    "seera_hip_unpooling_bwd": ([_vp, _vp] + [_i] * 6, _i),
+    **{f"seera_hip_{n}": ([_vp, _vp, _i, _i, _vp], _i)
+       for n in ("sum_fwd", "mean_fwd", "max_fwd", "min_fwd", "argmax_fwd", "argmin_fwd",
+                 "sum_bwd", "mean_bwd")},
+    "seera_hip_max_bwd": ([_vp] * 4 + [_i, _i, _vp], _i),
+    "seera_hip_min_bwd": ([_vp] * 4 + [_i, _i, _vp], _i),
+    **{f"seera_hip_{n}": ([_vp, _f, _i], _i)
+       for n in ("scaler_multiply_f", "scaler_add_f", "power_of")},
+    **{f"seera_hip_{n}": ([_vp, _vp, _vp, _i], _i)
+       for n in ("elemadd", "elemsub", "elemdiv", "elemmult")},
+    "seera_hip_broadcast_add_4d": ([_vp] * 3 + [_i] * 8, _i),
+    "seera_hip_broadcast_mul_4d": ([_vp] * 3 + [_i] * 8, _i),
 }
 
 _lib = None

@@ -568,6 +568,14 @@ int seera_hip_graph_capture_end(void* stream, void** graph_exec) {
         const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+        // The graph holds the workspace addresses it was captured with: from
+        // now on a grown workspace keeps its old buffer until this graph (and
+        // every other live one on the device) is destroyed.
+        const int st = graph_created(exec);
+        if (st != SEERA_OK) {
+            (void)hipGraphExecDestroy(exec);
+            return st;
+        }
         *graph_exec = exec;
         return (int)SEERA_OK;
     });
@@ -581,7 +589,14 @@ int seera_hip_graph_launch(void* graph_exec, void* stream) {
 }
 int seera_hip_graph_destroy(void* graph_exec) {
     return guarded([&] {
-        if (graph_exec) SEERA_HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+        if (!graph_exec) return (int)SEERA_OK;
+        SEERA_HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+        return graph_destroyed(graph_exec);
+    });
+}
+int seera_hip_workspace_stats(size_t* held_bytes, size_t* retired_buffers) {
+    return guarded([&] {
+        workspace_stats(held_bytes, retired_buffers);
         return (int)SEERA_OK;
     });
 }

@@ -338,7 +338,7 @@ int conv_bias_grad(const float* dY, float* db, int B, int F, int HW, hipStream_t
     const int per = (B + G - 1) / G;
     const int Gu = (B + per - 1) / per;  // groups that hold an image
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(float) * (size_t)F * Gu, &ws));
+    SEERA_TRY(workspace(sizeof(float) * (size_t)F * Gu, &ws, st));
     float* part = static_cast<float*>(ws);
     if (HW % 4 == 0 && aligned16(dY))
         hipLaunchKernelGGL(conv_bias_partial<true>, dim3((unsigned)(F * Gu)), dim3(kCbThreads), 0,
@@ -367,7 +367,7 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     // Gather path: any width, any stride.
     void* ws = nullptr;
     const int64_t wn = (int64_t)F * C * R * S;
-    SEERA_TRY(workspace(sizeof(float) * (size_t)std::max<int64_t>(wn, 1), &ws));
+    SEERA_TRY(workspace(sizeof(float) * (size_t)std::max<int64_t>(wn, 1), &ws, st));
     float* Wt = static_cast<float*>(ws);
     if (wn > 0) {
         hipLaunchKernelGGL(relayout_dgrad_weight, dim3((unsigned)((wn + 255) / 256)), dim3(256), 0,

@@ -1026,7 +1026,7 @@ int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H
     const int64_t wsz = (int64_t)a.nftiles * a.nchunks * R * S * 2048;
     if (wsz > 0x7fffffff) return SEERA_OK;  // prep kernel indexes in 32 bits
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(half_t) * (size_t)wsz, &ws));
+    SEERA_TRY(workspace(sizeof(half_t) * (size_t)wsz, &ws, st));
     a.wk = static_cast<const half_t*>(ws);
     hipLaunchKernelGGL(prep_fwd_weights, dim3((unsigned)((wsz + 255) / 256)), dim3(256), 0, st, Wt,
                        static_cast<half_t*>(ws), F, C, R, S, a.nchunks, (int)wsz);
@@ -1081,7 +1081,7 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
     if (!plan_tile(a)) return SEERA_OK;
     if (woff > 0x7fffffff) return SEERA_OK;  // prep kernel indexes in 32 bits
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(half_t) * (size_t)std::max<int64_t>(woff, 1), &ws));
+    SEERA_TRY(workspace(sizeof(half_t) * (size_t)std::max<int64_t>(woff, 1), &ws, st));
     a.wk = static_cast<const half_t*>(ws);
     if (woff > 0) {
         // One launch for every phase's weights (they sit back to back in ws).
@@ -1184,7 +1184,7 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     a.nsplit = ceil_div(a.items, a.ips);
     const int ntot = a.CT * R * S;
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(float) * (size_t)tiles * a.nsplit * 64 * ntot, &ws));
+    SEERA_TRY(workspace(sizeof(float) * (size_t)tiles * a.nsplit * 64 * ntot, &ws, st));
     a.part = static_cast<float*>(ws);
     hipError_t e;
     if (sw == 1) e = nch == 2 ? launch_wgrad_sw<1, 2>(a, ngw, st) : launch_wgrad_sw<1, 1>(a, ngw, st);

@@ -426,7 +426,7 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     a.nstrip = (Ho + a.L - 1) / a.L;
     a.nsplit = B * a.nstrip;
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(float) * (size_t)ntiles * a.nsplit * 64 * kTile * R * S, &ws));
+    SEERA_TRY(workspace(sizeof(float) * (size_t)ntiles * a.nsplit * 64 * kTile * R * S, &ws, st));
     a.part = static_cast<float*>(ws);
     hipError_t e;
     switch (R) {

@@ -152,25 +152,34 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
     return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1, EPI>{}), pl, st);
 }
 
-// LDS-tiled transpose of one [rows, cols] slice per blockIdx.z; 64x64 tiles,
-// coalesced reads and writes, +1 padding against bank conflicts.
+// LDS-tiled transposes of `batch` [rows, cols] slices; 64x64 tiles, coalesced
+// reads and writes, +1 padding against bank conflicts. Column tiles are on
+// blockIdx.x; row tiles and slices loop over blockIdx.y / blockIdx.z in steps
+// of the grid, so any extent fits the 65535 limit of those grid dimensions.
 __global__ __launch_bounds__(256) void transpose_tiles(const float* __restrict__ in,
-                                                       float* __restrict__ out, int rows,
-                                                       int cols) {
+                                                       float* __restrict__ out, int batch,
+                                                       int rows, int cols) {
     __shared__ float t[64][65];
     const int64_t slice = (int64_t)rows * cols;
-    in += blockIdx.z * slice;
-    out += blockIdx.z * slice;
-    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int nby = (rows + 63) / 64;
+    const int c0 = blockIdx.x * 64;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int i = ty; i < 64; i += 4) {
-        const int r = r0 + i, c = c0 + tx;
-        if (r < rows && c < cols) t[i][tx] = in[(int64_t)r * cols + c];
-    }
-    __syncthreads();
-    for (int i = ty; i < 64; i += 4) {
-        const int c = c0 + i, r = r0 + tx;
-        if (c < cols && r < rows) out[(int64_t)c * rows + r] = t[tx][i];
+    for (int z = blockIdx.z; z < batch; z += gridDim.z) {
+        const float* src = in + z * slice;
+        float* dst = out + z * slice;
+        for (int by = blockIdx.y; by < nby; by += gridDim.y) {
+            const int r0 = by * 64;
+            for (int i = ty; i < 64; i += 4) {
+                const int r = r0 + i, c = c0 + tx;
+                if (r < rows && c < cols) t[i][tx] = src[(int64_t)r * cols + c];
+            }
+            __syncthreads();
+            for (int i = ty; i < 64; i += 4) {
+                const int c = c0 + i, r = r0 + tx;
+                if (c < cols && r < rows) dst[(int64_t)c * rows + r] = t[tx][i];
+            }
+            __syncthreads();  // the tile is rewritten by the next step
+        }
     }
 }
 
@@ -178,30 +187,38 @@ __global__ __launch_bounds__(256) void transpose_tiles(const float* __restrict__
 // both tensors 16-byte aligned: a thread reads 4 consecutive columns of one
 // input row and writes 4 consecutive columns (input rows) of one output row.
 __global__ __launch_bounds__(256) void transpose_tiles4(const float* __restrict__ in,
-                                                        float* __restrict__ out, int rows,
-                                                        int cols) {
+                                                        float* __restrict__ out, int batch,
+                                                        int rows, int cols) {
     __shared__ float t[64][65];
     const int64_t slice = (int64_t)rows * cols;
-    in += blockIdx.z * slice;
-    out += blockIdx.z * slice;
-    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int nby = (rows + 63) / 64;
+    const int c0 = blockIdx.x * 64;
     const int q = threadIdx.x & 15, ty = threadIdx.x >> 4;  // quad column, row group
-    for (int i = ty; i < 64; i += 16) {
-        const int r = r0 + i, c = c0 + 4 * q;
-        if (r < rows && c < cols) {  // c < cols means all 4 (cols % 4 == 0)
-            const float4 v = *reinterpret_cast<const float4*>(in + (int64_t)r * cols + c);
-            t[i][4 * q] = v.x;
-            t[i][4 * q + 1] = v.y;
-            t[i][4 * q + 2] = v.z;
-            t[i][4 * q + 3] = v.w;
+    for (int z = blockIdx.z; z < batch; z += gridDim.z) {
+        const float* src = in + z * slice;
+        float* dst = out + z * slice;
+        for (int by = blockIdx.y; by < nby; by += gridDim.y) {
+            const int r0 = by * 64;
+            for (int i = ty; i < 64; i += 16) {
+                const int r = r0 + i, c = c0 + 4 * q;
+                if (r < rows && c < cols) {  // c < cols means all 4 (cols % 4 == 0)
+                    const float4 v =
+                        *reinterpret_cast<const float4*>(src + (int64_t)r * cols + c);
+                    t[i][4 * q] = v.x;
+                    t[i][4 * q + 1] = v.y;
+                    t[i][4 * q + 2] = v.z;
+                    t[i][4 * q + 3] = v.w;
+                }
+            }
+            __syncthreads();
+            for (int i = ty; i < 64; i += 16) {
+                const int c = c0 + i, r = r0 + 4 * q;
+                if (c < cols && r < rows)
+                    *reinterpret_cast<float4*>(dst + (int64_t)c * rows + r) = make_float4(
+                        t[4 * q][i], t[4 * q + 1][i], t[4 * q + 2][i], t[4 * q + 3][i]);
+            }
+            __syncthreads();
         }
-    }
-    __syncthreads();
-    for (int i = ty; i < 64; i += 16) {
-        const int c = c0 + i, r = r0 + 4 * q;
-        if (c < cols && r < rows)
-            *reinterpret_cast<float4*>(out + (int64_t)c * rows + r) =
-                make_float4(t[4 * q][i], t[4 * q + 1][i], t[4 * q + 2][i], t[4 * q + 3][i]);
     }
 }
 
@@ -281,13 +298,13 @@ int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* 
 
 int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st) {
     if (batch == 0 || rows == 0 || cols == 0) return SEERA_OK;
-    dim3 grid((cols + 63) / 64, (rows + 63) / 64, batch);
-    if (grid.y > 65535 || grid.z > 65535)
-        return fail(SEERA_ERR_INVALID_ARGUMENT, "transpose extent too large");
+    // Column tiles on x (ceil(cols / 64) < 2^26); row tiles and slices are
+    // looped in the kernel beyond 65535 each.
+    dim3 grid((cols + 63) / 64, std::min((rows + 63) / 64, 65535), std::min(batch, 65535));
     if (rows % 4 == 0 && cols % 4 == 0 && aligned16(in) && aligned16(out))
-        hipLaunchKernelGGL(transpose_tiles4, grid, dim3(256), 0, st, in, out, rows, cols);
+        hipLaunchKernelGGL(transpose_tiles4, grid, dim3(256), 0, st, in, out, batch, rows, cols);
     else
-        hipLaunchKernelGGL(transpose_tiles, grid, dim3(256), 0, st, in, out, rows, cols);
+        hipLaunchKernelGGL(transpose_tiles, grid, dim3(256), 0, st, in, out, batch, rows, cols);
     SEERA_HIP_TRY(hipGetLastError());
     return SEERA_OK;
 }

@@ -51,4 +51,41 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
 int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
                int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
 
+// ---- tensor_ops.hip: the reference's element-wise, activation, softmax,
+// broadcast, unpooling and reduction functions ----
+enum {
+    kActFwdRelu, kActFwdSigmoid, kActFwdTanh, kActFwdLog, kActFwdExp, kActFwdAbs, kActFwdSqrt,
+    kActFwdPow, kActFwdClip
+};
+// out = f(x), grad = f'(x) over n elements; p0 = exponent (pow) or lo (clip),
+// p1 = hi (clip).
+int activation_fwd(int kind, const float* x, float* out, float* grad, int64_t n, float p0,
+                   float p1, hipStream_t st);
+enum { kElemAdd, kElemSub, kElemMul, kElemDiv };
+// C = A op B over n elements.
+int elementwise(int op, const float* A, const float* B, float* C, int64_t n, hipStream_t st);
+enum { kScalarMul, kScalarAdd, kScalarPow };
+// p = p op k in place.
+int scalar_inplace(int op, float* p, float k, int64_t n, hipStream_t st);
+// C = A + B (or A * B) with 4-D broadcasting of extent-1 axes.
+int broadcast_4d(bool mul, const float* A, const float* B, float* C, const int a[4],
+                 const int b[4], hipStream_t st);
+// Nearest-neighbour upsample of [B, C, H, W] by (sh, sw), or its backward
+// (dst [B, C, H, W] = block sums of src [B, C, H*sh, W*sw]).
+int unpool(bool backward, const float* src, float* dst, int B, int C, int H, int W, int sh,
+           int sw, hipStream_t st);
+// Row softmax of a [N, C] into out, or (vjp) out = a * (b - <a, b>) per row
+// with a = softmax output, b = dout.
+int softmax(bool vjp, const float* a, const float* b, float* out, int N, int C, hipStream_t st);
+enum {
+    kRedSum, kRedMean, kRedMax, kRedMin, kRedArgmax, kRedArgmin, kRedSumBwd, kRedMeanBwd,
+    kRedMaxBwd, kRedMinBwd
+};
+// Reduction of axis `dim` of a row-major tensor with host extents dims[ndims]:
+//   forward kinds: A -> out (float, or int for argmax / argmin)
+//   kRedSumBwd / kRedMeanBwd: dOut -> out (= dA)
+//   kRedMaxBwd / kRedMinBwd: dOut, A (forward input), Y (forward output) -> out
+int reduce_axis(int kind, const float* A, const float* Y, const float* dOut, void* out, int ndims,
+                int dim, const int* dims, hipStream_t st);
+
 }  // namespace seera

@@ -135,7 +135,7 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
     const int64_t final_ld = p.ldc;
     if (pl.splits > 1) {
         void* ws = nullptr;
-        SEERA_TRY(workspace(sizeof(float) * (size_t)pl.splits * p.M * p.N, &ws));
+        SEERA_TRY(workspace(sizeof(float) * (size_t)pl.splits * p.M * p.N, &ws, st));
         p.C = static_cast<float*>(ws);
         p.ldc = p.N;
         p.split_stride = (int64_t)p.M * p.N;

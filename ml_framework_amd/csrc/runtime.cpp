@@ -1,6 +1,7 @@
 // runtime.cpp -- error reporting, the per-device workspace and the caching
 // device allocator behind seera_hip_malloc / seera_hip_free.
 #include "runtime.h"
+#include "workspace_pool.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -17,13 +18,36 @@ namespace seera {
 namespace {
 thread_local char g_msg[512] = "";
 
-struct DeviceScratch {
-    void* ptr = nullptr;
-    size_t bytes = 0;
+// Workspaces: one per (device, stream), kept and grown by WorkspacePool
+// (workspace_pool.h) over the HIP backend below.
+struct HipBackend {
+    int alloc(int, size_t bytes, void** out) {
+        SEERA_HIP_TRY(hipMalloc(out, bytes));
+        return SEERA_OK;
+    }
+    int release(int, void* p) {
+        SEERA_HIP_TRY(hipFree(p));
+        return SEERA_OK;
+    }
+    int sync(int dev) {
+        int cur = 0;
+        SEERA_HIP_TRY(hipGetDevice(&cur));
+        if (cur != dev) SEERA_HIP_TRY(hipSetDevice(dev));
+        const hipError_t e = hipDeviceSynchronize();
+        if (cur != dev) SEERA_HIP_TRY(hipSetDevice(cur));
+        SEERA_HIP_TRY(e);
+        return SEERA_OK;
+    }
 };
-constexpr int kMaxDevices = 64;
-DeviceScratch g_scratch[kMaxDevices];
+HipBackend g_hip_backend;
+WorkspacePool<HipBackend> g_pool(g_hip_backend);
 std::mutex g_scratch_mu;
+
+// A caller-supplied scratch region that workspace() hands out instead of the
+// library's own buffers (seera_hip_matmul_noalloc), per host thread.
+thread_local void* g_fixed_ptr = nullptr;
+thread_local size_t g_fixed_bytes = 0;
+thread_local const char* g_fixed_owner = nullptr;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -45,27 +69,63 @@ void clear_error() { g_msg[0] = 0; }
 
 const char* last_error() { return g_msg; }
 
-int workspace(size_t bytes, void** out) {
+FixedWorkspace::FixedWorkspace(void* ptr, size_t bytes, const char* owner) {
+    g_fixed_ptr = ptr;
+    g_fixed_bytes = bytes;
+    g_fixed_owner = owner;
+}
+FixedWorkspace::~FixedWorkspace() {
+    g_fixed_ptr = nullptr;
+    g_fixed_bytes = 0;
+    g_fixed_owner = nullptr;
+}
+
+int workspace(size_t bytes, void** out, hipStream_t st) {
+    *out = nullptr;
+    if (g_fixed_owner) {
+        if (bytes > g_fixed_bytes)
+            return fail(SEERA_ERR_INVALID_ARGUMENT,
+                        "%s: this call needs %zu bytes of scratch, above its fixed maximum of %zu",
+                        g_fixed_owner, bytes, g_fixed_bytes);
+        *out = g_fixed_ptr;
+        return SEERA_OK;
+    }
     int dev = 0;
     SEERA_HIP_TRY(hipGetDevice(&dev));
-    if (dev < 0 || dev >= kMaxDevices) return fail(SEERA_ERR_HIP, "device id %d out of range", dev);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    DeviceScratch& s = g_scratch[dev];
-    if (bytes > s.bytes) {
-        if (s.ptr) {
-            // Kernels queued earlier may still read the old buffer.
-            SEERA_HIP_TRY(hipDeviceSynchronize());
-            SEERA_HIP_TRY(hipFree(s.ptr));
-            s.ptr = nullptr;
-            s.bytes = 0;
-        }
-        // Round up to 1 MiB so small growth steps do not reallocate.
-        const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-        SEERA_HIP_TRY(hipMalloc(&s.ptr, want));
-        s.bytes = want;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        // Not a capturable stream (the query is refused, e.g. for the legacy
+        // null stream in some runtime states): it is not being captured.
+        (void)hipGetLastError();
+        cap = hipStreamCaptureStatusNone;
     }
-    *out = s.ptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    const int e = g_pool.get(dev, st, bytes, cap != hipStreamCaptureStatusNone, out);
+    if (e == WorkspacePool<HipBackend>::kGrowUnderCapture)
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "the workspace must grow to %zu bytes during stream capture: make one eager "
+                    "call of the same sizes on this stream before capturing",
+                    bytes);
+    return e;
+}
+
+int graph_created(void* exec) {
+    int dev = 0;
+    SEERA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    g_pool.graph_created(exec, dev);
     return SEERA_OK;
+}
+
+int graph_destroyed(void* exec) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_pool.graph_destroyed(exec);
+}
+
+void workspace_stats(size_t* held, size_t* retired_count) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (held) *held = g_pool.held_bytes();
+    if (retired_count) *retired_count = g_pool.retired_count();
 }
 
 // ---------------------------------------------------------------------------
@@ -117,8 +177,16 @@ int release_cached(int dev) {
         int cur = 0;
         SEERA_HIP_TRY(hipGetDevice(&cur));
         SEERA_HIP_TRY(hipSetDevice(it->first.first));
-        for (void* p : it->second) {
-            SEERA_HIP_TRY(hipFree(p));
+        // Erase each block as it is freed: after a failed hipFree the list
+        // holds exactly the blocks that are still allocated.
+        std::vector<void*>& blocks = it->second;
+        while (!blocks.empty()) {
+            const hipError_t e = hipFree(blocks.back());
+            if (e != hipSuccess) {
+                (void)hipSetDevice(cur);
+                return fail_hip(e, "hipFree of a cached block");
+            }
+            blocks.pop_back();
             g_cached_bytes -= it->first.second;
         }
         SEERA_HIP_TRY(hipSetDevice(cur));

@@ -27,11 +27,32 @@ void clear_error();
         if (seera_s_ != SEERA_OK) return seera_s_; \
     } while (0)
 
-// Device scratch owned by the library (split-K partials, re-laid-out weights).
-// Grows on demand and is kept until process exit. A grow synchronizes the
-// device first so no queued kernel still uses the old buffer. Not safe for
-// concurrent calls from several host threads on one device.
-int workspace(size_t bytes, void** out);
+// Device scratch owned by the library (split-K partials, re-laid-out weights,
+// dW and bias partials): one buffer per (device, stream), so calls on two
+// streams never share one. Grows on demand and is kept until process exit; a
+// grow synchronizes the device first so no queued kernel still uses the old
+// buffer, and while a HIP graph is live on the device the old buffer is kept
+// (a replay still writes to it) until the device's last graph is destroyed.
+// Growing while `st` is being captured fails with SEERA_ERR_INVALID_ARGUMENT.
+int workspace(size_t bytes, void** out, hipStream_t st);
+
+// While alive, workspace() on this host thread hands out [ptr, ptr + bytes)
+// instead of the library's buffers and fails (naming `owner`) for requests
+// above `bytes`. Used by the entry point that must not allocate.
+class FixedWorkspace {
+public:
+    FixedWorkspace(void* ptr, size_t bytes, const char* owner);
+    ~FixedWorkspace();
+    FixedWorkspace(const FixedWorkspace&) = delete;
+    FixedWorkspace& operator=(const FixedWorkspace&) = delete;
+};
+
+// Graph bookkeeping for the workspace rule above (capi.cpp calls these when
+// an executable graph is instantiated and destroyed).
+int graph_created(void* exec);
+int graph_destroyed(void* exec);
+// Bytes held by workspaces and the number of retired (graph-pinned) buffers.
+void workspace_stats(size_t* held, size_t* retired_count);
 
 // Caching device allocator behind seera_hip_malloc / seera_hip_free (size
 // classes per device; see runtime.cpp). A free synchronizes the device first

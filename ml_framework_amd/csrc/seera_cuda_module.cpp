@@ -182,6 +182,154 @@ PYBIND11_MODULE(seera_cuda, m) {
           },
           "(bytes in live allocations, bytes cached for reuse)");
 
+    // ---- activations (cuda_bindings.cpp:176-239): x -> out, grad ----
+#define SEERA_ACT(name, fn, doc)                                                          \
+    m.def(name,                                                                           \
+          [](uintptr_t x, uintptr_t out, uintptr_t grad, int size) {                     \
+              check(fn(dev<const float>(x), dev<float>(out), dev<float>(grad), size));   \
+          },                                                                              \
+          doc)
+    SEERA_ACT("cuda_relu_fwd", seera_hip_relu_fwd, "ReLU forward: x -> out, grad (GPU ptrs)");
+    SEERA_ACT("cuda_sigmoid_fwd", seera_hip_sigmoid_fwd, "Sigmoid forward (GPU ptrs)");
+    SEERA_ACT("cuda_tanh_fwd", seera_hip_tanh_fwd, "Tanh forward (GPU ptrs)");
+    SEERA_ACT("cuda_log_fwd", seera_hip_log_fwd, "Log forward (GPU ptrs)");
+    SEERA_ACT("cuda_exp_fwd", seera_hip_exp_fwd, "Exp forward (GPU ptrs)");
+    SEERA_ACT("cuda_abs_fwd", seera_hip_abs_fwd, "Abs forward (GPU ptrs)");
+    SEERA_ACT("cuda_sqrt_fwd", seera_hip_sqrt_fwd, "Sqrt forward (GPU ptrs)");
+#undef SEERA_ACT
+    m.def("cuda_pow_fwd",
+          [](uintptr_t x, float exponent, uintptr_t out, uintptr_t grad, int size) {
+              check(seera_hip_pow_fwd(dev<const float>(x), exponent, dev<float>(out),
+                                      dev<float>(grad), size));
+          },
+          "Pow forward (GPU ptrs)");
+    m.def("cuda_clip_fwd",
+          [](uintptr_t x, float lo, float hi, uintptr_t out, uintptr_t grad, int size) {
+              check(seera_hip_clip_fwd(dev<const float>(x), lo, hi, dev<float>(out),
+                                       dev<float>(grad), size));
+          },
+          "Clip forward (GPU ptrs)");
+
+    // ---- softmax (cuda_bindings.cpp:243-253) ----
+    m.def("cuda_softmax_fwd",
+          [](uintptr_t x, uintptr_t out, int N, int C) {
+              check(seera_hip_softmax_fwd(dev<const float>(x), dev<float>(out), N, C));
+          },
+          "Softmax forward: x[N,C] -> out[N,C] (GPU ptrs)");
+    m.def("cuda_softmax_vjp",
+          [](uintptr_t s, uintptr_t dout, uintptr_t dx, int N, int C) {
+              check(seera_hip_softmax_vjp(dev<const float>(s), dev<const float>(dout),
+                                          dev<float>(dx), N, C));
+          },
+          "Softmax VJP backward (GPU ptrs)");
+
+    // ---- unpooling (cuda_bindings.cpp:358-370) ----
+    m.def("cuda_unpooling_fwd",
+          [](uintptr_t inp, uintptr_t out, int batchN, int C, int H, int W, int sh, int sw) {
+              check(seera_hip_unpooling_fwd(dev<const float>(inp), dev<float>(out), batchN, C, H,
+                                            W, sh, sw));
+          },
+          "Unpooling (nearest upsample) forward (GPU ptrs)");
+    m.def("cuda_unpooling_bwd",
+          [](uintptr_t dout, uintptr_t dx, int batchN, int C, int H, int W, int sh, int sw) {
+              check(seera_hip_unpooling_bwd(dev<const float>(dout), dev<float>(dx), batchN, C, H,
+                                            W, sh, sw));
+          },
+          "Unpooling backward (GPU ptrs)");
+
+    // ---- reductions (cuda_bindings.cpp:376-457); dimarr is a host int32
+    // array with ndims entries ----
+    auto dims_ok = [](const arr_i& d, int ndims) {
+        if (ndims < 0 || d.size() < ndims)
+            throw std::invalid_argument("seera_cuda: dimarr holds fewer than ndims extents");
+        return d.data();
+    };
+#define SEERA_RED(name, fn, T, doc)                                                        \
+    m.def(name,                                                                            \
+          [dims_ok](uintptr_t A, uintptr_t out, int ndims, int dim, arr_i dimarr) {        \
+              check(fn(dev<const float>(A), dev<T>(out), ndims, dim, dims_ok(dimarr, ndims))); \
+          },                                                                               \
+          doc)
+    SEERA_RED("cuda_sum_fwd", seera_hip_sum_fwd, float,
+              "Sum reduction forward (A, out: GPU ptrs; dimarr: numpy)");
+    SEERA_RED("cuda_mean_fwd", seera_hip_mean_fwd, float,
+              "Mean reduction forward (A, out: GPU ptrs; dimarr: numpy)");
+    SEERA_RED("cuda_max_fwd", seera_hip_max_fwd, float,
+              "Max reduction forward (A, out: GPU ptrs; dimarr: numpy)");
+    SEERA_RED("cuda_min_fwd", seera_hip_min_fwd, float,
+              "Min reduction forward (A, out: GPU ptrs; dimarr: numpy)");
+    SEERA_RED("cuda_argmax_fwd", seera_hip_argmax_fwd, int,
+              "Argmax reduction forward (A: float GPU, out: int GPU; dimarr: numpy)");
+    SEERA_RED("cuda_argmin_fwd", seera_hip_argmin_fwd, int,
+              "Argmin reduction forward (A: float GPU, out: int GPU; dimarr: numpy)");
+    SEERA_RED("cuda_sum_bwd", seera_hip_sum_bwd, float,
+              "Sum reduction backward (GPU ptrs; dimarr: numpy)");
+    SEERA_RED("cuda_mean_bwd", seera_hip_mean_bwd, float,
+              "Mean reduction backward (GPU ptrs; dimarr: numpy)");
+#undef SEERA_RED
+    m.def("cuda_max_bwd",
+          [dims_ok](uintptr_t dOut, uintptr_t fwdInput, uintptr_t fwdOutput, uintptr_t dA,
+                    int ndims, int dim, arr_i dimarr) {
+              check(seera_hip_max_bwd(dev<const float>(dOut), dev<const float>(fwdInput),
+                                      dev<const float>(fwdOutput), dev<float>(dA), ndims, dim,
+                                      dims_ok(dimarr, ndims)));
+          },
+          "Max reduction backward (GPU ptrs; dimarr: numpy)");
+    m.def("cuda_min_bwd",
+          [dims_ok](uintptr_t dOut, uintptr_t fwdInput, uintptr_t fwdOutput, uintptr_t dA,
+                    int ndims, int dim, arr_i dimarr) {
+              check(seera_hip_min_bwd(dev<const float>(dOut), dev<const float>(fwdInput),
+                                      dev<const float>(fwdOutput), dev<float>(dA), ndims, dim,
+                                      dims_ok(dimarr, ndims)));
+          },
+          "Min reduction backward (GPU ptrs; dimarr: numpy)");
+
+    // ---- scalar ops (cuda_bindings.cpp:461-465, 479-481), in place ----
+    m.def("cuda_scaler_multiply_f",
+          [](uintptr_t arr, float k, int total_elements) {
+              check(seera_hip_scaler_multiply_f(dev<float>(arr), k, total_elements));
+          },
+          "Scalar multiply float (GPU ptr)");
+    m.def("cuda_scaler_add_f",
+          [](uintptr_t arr, float k, int total_elements) {
+              check(seera_hip_scaler_add_f(dev<float>(arr), k, total_elements));
+          },
+          "Scalar add float (GPU ptr)");
+    m.def("cuda_power_of",
+          [](uintptr_t arr, float k, int total_elements) {
+              check(seera_hip_power_of(dev<float>(arr), k, total_elements));
+          },
+          "Element-wise power arr = arr ** k (GPU ptr)");
+
+    // ---- element-wise (cuda_bindings.cpp:486-512) ----
+#define SEERA_ELEM(name, fn, doc)                                                     \
+    m.def(name,                                                                       \
+          [](uintptr_t A, uintptr_t B, uintptr_t C, int size) {                      \
+              check(fn(dev<const float>(A), dev<const float>(B), dev<float>(C), size)); \
+          },                                                                          \
+          doc)
+    SEERA_ELEM("cuda_elemadd", seera_hip_elemadd, "Elementwise add (float)");
+    SEERA_ELEM("cuda_elemsub", seera_hip_elemsub, "Elementwise sub (float)");
+    SEERA_ELEM("cuda_elemdiv", seera_hip_elemdiv, "Elementwise div (float)");
+    SEERA_ELEM("cuda_elemmult", seera_hip_elemmult, "Elementwise mul (float)");
+#undef SEERA_ELEM
+
+    // ---- 4-D broadcast (cuda_bindings.cpp:518-532) ----
+    m.def("broadcast_add_4d",
+          [](uintptr_t A, uintptr_t B, uintptr_t C, int aN, int aC, int aH, int aW, int bN,
+             int bC, int bH, int bW) {
+              check(seera_hip_broadcast_add_4d(dev<const float>(A), dev<const float>(B),
+                                               dev<float>(C), aN, aC, aH, aW, bN, bC, bH, bW));
+          },
+          "Broadcast add 4D (GPU ptrs)");
+    m.def("broadcast_mul_4d",
+          [](uintptr_t A, uintptr_t B, uintptr_t C, int aN, int aC, int aH, int aW, int bN,
+             int bC, int bH, int bW) {
+              check(seera_hip_broadcast_mul_4d(dev<const float>(A), dev<const float>(B),
+                                               dev<float>(C), aN, aC, aH, aW, bN, bC, bH, bW));
+          },
+          "Broadcast mul 4D (GPU ptrs)");
+
     // ---- transfers (cuda_bindings.cpp:73-170) ----
     m.def("to_device_f16", [](arr_f a) { return upload<float>(a); },
           "Upload float32 numpy -> float32 GPU buffer (reference name)");

@@ -82,7 +82,44 @@ REFERENCE_SIGNATURES = {
     "cuda_zeros_f": 1,                   # 474 (total_elements) -> device pointer
     "cuda_maxpool_fwd": 13,              # 338 (image, out, mask, N, C, H, W, R, S, ph, pw, sh, sw)
     "cuda_maxpool_bwd": 13,              # 346 (dout, mask, dX, N, C, H, W, R, S, ph, pw, sh, sw)
+    "cuda_relu_fwd": 4,                  # 176 (x, out, grad, size)
+    "cuda_sigmoid_fwd": 4,               # 183
+    "cuda_tanh_fwd": 4,                  # 190
+    "cuda_log_fwd": 4,                   # 197
+    "cuda_exp_fwd": 4,                   # 204
+    "cuda_abs_fwd": 4,                   # 211
+    "cuda_sqrt_fwd": 4,                  # 218
+    "cuda_pow_fwd": 5,                   # 225 (x, exponent, out, grad, size)
+    "cuda_clip_fwd": 6,                  # 232 (x, lo, hi, out, grad, size)
+    "cuda_softmax_fwd": 4,               # 243 (x, out, N, C)
+    "cuda_softmax_vjp": 5,               # 249 (s, dout, dx, N, C)
+    "cuda_unpooling_fwd": 8,             # 358 (inp, out, batchN, C, H, W, sh, sw)
+    "cuda_unpooling_bwd": 8,             # 365 (dout, dx, batchN, C, H, W, sh, sw)
+    "cuda_sum_fwd": 5,                   # 376 (A, out, ndims, dim, dimarr)
+    "cuda_mean_fwd": 5,                  # 384
+    "cuda_max_fwd": 5,                   # 392
+    "cuda_min_fwd": 5,                   # 400
+    "cuda_argmax_fwd": 5,                # 408
+    "cuda_argmin_fwd": 5,                # 416
+    "cuda_sum_bwd": 5,                   # 426 (dOut, dA, ndims, dim, dimarr)
+    "cuda_mean_bwd": 5,                  # 434
+    "cuda_max_bwd": 7,                   # 442 (dOut, fwdInput, fwdOutput, dA, ndims, dim, dimarr)
+    "cuda_min_bwd": 7,                   # 452
+    "cuda_scaler_multiply_f": 3,         # 461 (arr, k, total_elements)
+    "cuda_scaler_add_f": 3,              # 464
+    "cuda_power_of": 3,                  # 479
+    "cuda_elemadd": 4,                   # 486 (A, B, C, size)
+    "cuda_elemsub": 4,                   # 493
+    "cuda_elemdiv": 4,                   # 500
+    "cuda_elemmult": 4,                  # 507
+    "broadcast_add_4d": 11,              # 518 (A, B, C, aN, aC, aH, aW, bN, bC, bH, bW)
+    "broadcast_mul_4d": 11,              # 526
 }
+
+
+def test_reference_signature_table_is_complete():
+    """Every name cuda_bindings.cpp defines (60) is in the table."""
+    assert len(REFERENCE_SIGNATURES) == 60
 
 
 def _arity(fn):
@@ -176,3 +213,44 @@ def test_validation_fused_entry_points():
     assert st == capi.SEERA_ERR_INVALID_ARGUMENT, msg
     st, msg = _status("seera_hip_graph_launch", None, None)
     assert st == capi.SEERA_ERR_INVALID_ARGUMENT, msg
+
+
+@pytest.mark.parametrize("name,args,what", [
+    ("seera_hip_relu_fwd", (1, 1, 1, -1), "size"),
+    ("seera_hip_clip_fwd", (1, 0.0, 1.0, 1, 1, -3), "size"),
+    ("seera_hip_elemadd", (1, 1, 1, -1), "size"),
+    ("seera_hip_elemadd", (None, 1, 1, 4), "null"),
+    ("seera_hip_scaler_add_f", (1, 1.0, -2), "total_elements"),
+    ("seera_hip_softmax_fwd", (1, 1, -1, 4), "N and C"),
+    ("seera_hip_unpooling_fwd", (1, 1, 1, 1, 2, 2, 0, 2), "scale"),
+    ("seera_hip_unpooling_bwd", (1, 1, 1, -1, 2, 2, 2, 2), "negative"),
+    ("seera_hip_broadcast_add_4d", (1, 1, 1, 2, 3, 4, 5, 1, 2, 1, 1), "broadcast"),
+    ("seera_hip_broadcast_mul_4d", (1, 1, 1, 2, 3, 4, -5, 1, 1, 1, 1), "negative"),
+])
+def test_validation_tensor_ops(name, args, what):
+    st, msg = _status(name, *args)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and what in msg, (name, msg)
+
+
+def test_validation_reductions():
+    dims = (ctypes.c_int * 2)(2, 3)
+    st, msg = _status("seera_hip_sum_fwd", 1, 1, 2, 2, dims)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "dim" in msg, msg
+    st, msg = _status("seera_hip_max_fwd", 1, 1, 2, -1, dims)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "dim" in msg, msg
+    st, msg = _status("seera_hip_mean_bwd", 1, 1, 2, 0, None)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "extents" in msg, msg
+    empty = (ctypes.c_int * 2)(2, 0)
+    st, msg = _status("seera_hip_argmax_fwd", 1, 1, 2, 1, empty)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "empty" in msg, msg
+    st, msg = _status("seera_hip_max_bwd", 1, 1, None, 1, 2, 0, dims)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "null" in msg, msg
+
+
+def test_seera_cuda_reduction_checks_dimarr_length():
+    import ml_framework_amd
+    import numpy as np
+
+    mod = ml_framework_amd.seera_cuda()
+    with pytest.raises(ValueError, match="dimarr"):
+        mod.cuda_sum_fwd(1, 1, 3, 0, np.array([2, 3], np.int32))

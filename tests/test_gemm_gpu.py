@@ -240,3 +240,21 @@ def test_extreme_aspect_ratios(M, K, N, nb):
     rda, rdb = S.matmul_bwd(a, b, dc)
     assert_parity(da, rda, "dA")
     assert_parity(db, rdb, "dB")
+
+
+@pytest.mark.parametrize("rows,cols", [(5_000_000, 2), (2, 5_000_000), (4_194_305, 3)])
+def test_transpose_2d_beyond_grid_limit(rows, cols):
+    """Row tiles beyond the 65535 grid-y limit (the reference's 1-D grid
+    accepts any count: GEMM.cu:229-235)."""
+    a = np.random.default_rng(rows).standard_normal((rows, cols)).astype(np.float32)
+    with DeviceBuffer.from_array(a) as pi, DeviceBuffer(a.nbytes) as po:
+        capi.call("seera_hip_transpose_2d", pi.ptr, po.ptr, rows, cols)
+        assert np.array_equal(po.to_array((cols, rows)), a.T)
+
+
+def test_transpose_3d_many_slices():
+    """More slices than the 65535 grid-z limit."""
+    a = np.random.default_rng(9).standard_normal((70_000, 3, 2)).astype(np.float32)
+    with DeviceBuffer.from_array(a) as pi, DeviceBuffer(a.nbytes) as po:
+        capi.call("seera_hip_transpose_3d", pi.ptr, po.ptr, 70_000, 3, 2)
+        assert np.array_equal(po.to_array((70_000, 2, 3)), a.transpose(0, 2, 1))

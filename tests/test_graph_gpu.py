@@ -148,3 +148,131 @@ def test_conv_pool_layer_graph(lib, stream):
 
 def test_capture_needs_a_created_stream(lib):
     assert lib.seera_hip_graph_capture_begin(None) == capi.SEERA_ERR_INVALID_ARGUMENT
+
+
+def _stats(lib):
+    held, retired = ctypes.c_size_t(), ctypes.c_size_t()
+    capi.check(lib.seera_hip_workspace_stats(ctypes.byref(held), ctypes.byref(retired)))
+    return held.value, retired.value
+
+
+def _splitk_gemm(lib, a, b, c, M, N, K, stream):
+    # M, N small against K: the planner splits K and the partials go to the
+    # stream's workspace.
+    capi.check(lib.seera_hip_matmul_async(a.ptr, b.ptr, c.ptr, M, N, K, 1, stream))
+
+
+def test_replay_after_workspace_growth(lib, stream):
+    """A graph keeps the workspace address it was captured with. An eager
+    call that grows the stream's workspace between replays must not free that
+    buffer: the old one is retired until the graph is destroyed, and every
+    replay still equals the eager result bit for bit."""
+    r = np.random.default_rng(3)
+    K = 8192
+    a = DeviceBuffer.from_array(r.uniform(-1, 1, (64, K)).astype(np.float32))
+    b = DeviceBuffer.from_array(r.uniform(-1, 1, (K, 64)).astype(np.float32))
+    c = DeviceBuffer(64 * 64 * 4)
+    a2 = DeviceBuffer.from_array(r.uniform(-1, 1, (256, K)).astype(np.float32))
+    b2 = DeviceBuffer.from_array(r.uniform(-1, 1, (K, 256)).astype(np.float32))
+    c2 = DeviceBuffer(256 * 256 * 4)
+    _splitk_gemm(lib, a, b, c, 64, 64, K, stream)  # sizes the workspace
+    capi.check(lib.seera_hip_stream_synchronize(stream))
+    want = c.to_array((64, 64))
+    _, retired0 = _stats(lib)
+    g = _capture(lib, stream, lambda: _splitk_gemm(lib, a, b, c, 64, 64, K, stream))
+    try:
+        for rep in range(3):
+            # 16x the partials of the captured call: the workspace grows.
+            _splitk_gemm(lib, a2, b2, c2, 256, 256, K, stream)
+            capi.check(lib.seera_hip_stream_synchronize(stream))
+            if rep == 0:
+                assert _stats(lib)[1] >= retired0 + 1, "old workspace was not retired"
+            c.fill(0x7F)
+            capi.check(lib.seera_hip_graph_launch(g, stream))
+            capi.check(lib.seera_hip_stream_synchronize(stream))
+            assert np.array_equal(c.to_array((64, 64)), want), rep
+    finally:
+        capi.check(lib.seera_hip_graph_destroy(g))
+    assert _stats(lib)[1] == retired0, "retired workspaces not released with the graph"
+
+
+def test_growth_under_capture_is_a_clean_error(lib):
+    """A call that would have to grow its stream's workspace during capture
+    fails with SEERA_ERR_INVALID_ARGUMENT instead of recording a buffer a
+    later call could free."""
+    st = ctypes.c_void_p()
+    capi.check(lib.seera_hip_stream_create(ctypes.byref(st)))
+    r = np.random.default_rng(4)
+    K = 4096
+    a = DeviceBuffer.from_array(r.uniform(-1, 1, (32, K)).astype(np.float32))
+    b = DeviceBuffer.from_array(r.uniform(-1, 1, (K, 32)).astype(np.float32))
+    c = DeviceBuffer(32 * 32 * 4)
+    try:
+        capi.check(lib.seera_hip_graph_capture_begin(st.value))
+        status = lib.seera_hip_matmul_async(a.ptr, b.ptr, c.ptr, 32, 32, K, 1, st.value)
+        msg = lib.seera_hip_last_error().decode()
+        g = ctypes.c_void_p()
+        end = lib.seera_hip_graph_capture_end(st.value, ctypes.byref(g))
+        if end == capi.SEERA_OK:
+            capi.check(lib.seera_hip_graph_destroy(g.value))
+        assert status == capi.SEERA_ERR_INVALID_ARGUMENT and "capture" in msg, msg
+        # The same call outside capture sizes the workspace and succeeds.
+        capi.check(lib.seera_hip_matmul_async(a.ptr, b.ptr, c.ptr, 32, 32, K, 1, st.value))
+        capi.check(lib.seera_hip_stream_synchronize(st.value))
+    finally:
+        lib.seera_hip_stream_destroy(st.value)
+
+
+def test_async_calls_on_two_streams(lib):
+    """Split-K GEMMs and conv backward passes (dW partials) queued on two
+    streams at once: each stream has its own workspace, so both results equal
+    the same calls run one at a time."""
+    streams = []
+    for _ in range(2):
+        s = ctypes.c_void_p()
+        capi.check(lib.seera_hip_stream_create(ctypes.byref(s)))
+        streams.append(s.value)
+    r = np.random.default_rng(5)
+    K = 8192
+    gem = [(DeviceBuffer.from_array(r.uniform(-1, 1, (m, K)).astype(np.float32)),
+            DeviceBuffer.from_array(r.uniform(-1, 1, (K, m)).astype(np.float32)),
+            DeviceBuffer(m * m * 4), m) for m in (64, 96)]
+    N, C, H, W, F = 4, 16, 20, 20, 32
+    conv = []
+    for _ in range(2):
+        conv.append([DeviceBuffer.from_array(r.standard_normal(s).astype(np.float32))
+                     for s in ((F, C, 3, 3), (N, C, H, W), (N, F, H, W))] +
+                    [DeviceBuffer(N * C * H * W * 4), DeviceBuffer(F * C * 9 * 4)])
+
+    def queue(i, st):
+        a, b, c, m = gem[i]
+        capi.check(lib.seera_hip_matmul_async(a.ptr, b.ptr, c.ptr, m, m, K, 1, st))
+        w, x, dy, dx, dw = conv[i]
+        capi.check(lib.seera_hip_conv2d_bwd_async(w.ptr, x.ptr, dy.ptr, dx.ptr, dw.ptr, N, C, H,
+                                                  W, F, 3, 3, 1, 1, 1, 1, st))
+
+    def results(i):
+        return [gem[i][2].to_array((gem[i][3],) * 2), conv[i][3].to_array((N, C, H, W)),
+                conv[i][4].to_array((F, C, 3, 3))]
+
+    try:
+        want = []
+        for i in range(2):  # one at a time
+            queue(i, streams[i])
+            capi.check(lib.seera_hip_stream_synchronize(streams[i]))
+            want.append(results(i))
+        for rep in range(3):
+            for i in range(2):
+                for buf in (gem[i][2], conv[i][3], conv[i][4]):
+                    buf.fill(0x7F)
+            capi.check(lib.seera_hip_synchronize())
+            for i in range(2):  # both queued before either is waited for
+                queue(i, streams[i])
+            for s in streams:
+                capi.check(lib.seera_hip_stream_synchronize(s))
+            for i in range(2):
+                for j, (x, y) in enumerate(zip(results(i), want[i])):
+                    assert np.array_equal(x, y), (rep, i, j)
+    finally:
+        for s in streams:
+            lib.seera_hip_stream_destroy(s)

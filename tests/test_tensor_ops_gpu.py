@@ -1,0 +1,359 @@
+"""GPU parity of the reference's element-wise, activation, softmax,
+broadcast, unpooling and reduction functions (tensor_ops.hip) against
+oracle/tensor_ops.py, through the C ABI, and the cuTen Dense-layer call
+sequence through the seera_cuda module.
+
+Bars: bit-exact wherever the reference's arithmetic is exact IEEE fp32 in a
+fixed order (ReLU, abs, clip, sqrt, the element-wise and scalar add / sub /
+mul / div, broadcast, unpooling, every reduction and its backward); within
+4 ulp for the values of exp, log, tanh, sigmoid and pow (device math library
+against the host's), and rel 1e-5 / abs 1e-6 for their local gradients and
+for softmax (fp32 sums in another order).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from ml_framework_amd import capi
+from ml_framework_amd.capi import DeviceBuffer
+from oracle import fp16r
+from oracle import tensor_ops as T
+from tests.helpers import assert_parity
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+S = oracle.seera_cpp
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert capi.gpu_available(), "no HIP device visible"
+
+
+class Dev:
+    """A float32 array on the device at a chosen float offset from a
+    16-byte-aligned allocation (offset 1 exercises the scalar paths)."""
+
+    def __init__(self, a, offset=0, dtype=f32):
+        a = np.ascontiguousarray(a, dtype)
+        self.shape, self.dtype, self.n = a.shape, dtype, a.size
+        self.buf = DeviceBuffer((a.size + offset + 1) * 4)
+        self.ptr = self.buf.ptr + 4 * offset
+        if a.size:
+            capi.check(capi.load().seera_hip_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes))
+
+    @classmethod
+    def empty(cls, shape, offset=0, dtype=f32):
+        return cls(np.full(shape, np.nan if dtype == f32 else -7, dtype), offset, dtype)
+
+    def get(self):
+        out = np.empty(self.shape, self.dtype)
+        if out.size:
+            capi.check(capi.load().seera_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+
+def ulp_diff(a, b):
+    a = np.asarray(a, f32).ravel()
+    b = np.asarray(b, f32).ravel()
+    same = (a == b) | (np.isnan(a) & np.isnan(b))
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    d = np.abs(ia - ib)
+    return int(np.max(np.where(same, 0, d))) if a.size else 0
+
+
+def bit_equal(got, want, what=""):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, what
+    eq = (got.view(np.uint32) == want.view(np.uint32)) if got.dtype == f32 else (got == want)
+    if not np.all(eq):
+        i = np.flatnonzero(~eq.ravel())[0]
+        raise AssertionError(f"{what}: {int((~eq).sum())} differ, first at {i}: "
+                             f"{got.ravel()[i]!r} vs {want.ravel()[i]!r}")
+
+
+# (value exact, local gradient exact): sqrt and division are correctly
+# rounded on both sides; log's gradient is 1 / x.
+EXACT = {"relu": (True, True), "abs": (True, True), "clip": (True, True),
+         "sqrt": (True, True), "log": (False, True)}
+SIZES = [1, 3, 4, 1023, 4099, (1 << 16) + 3]
+
+
+@pytest.mark.parametrize("kind,p0,p1", [("relu", 0, 0), ("sigmoid", 0, 0), ("tanh", 0, 0),
+                                        ("log", 0, 0), ("exp", 0, 0), ("abs", 0, 0),
+                                        ("sqrt", 0, 0), ("pow", 2.0, 0), ("pow", 0.5, 0),
+                                        ("pow", -1.5, 0), ("clip", -0.5, 0.75)])
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_activation(kind, p0, p1, n, offset):
+    r = np.random.default_rng(n + offset)
+    x = (r.standard_normal(n) * 3).astype(f32)
+    if kind in ("log", "sqrt") or (kind == "pow" and p0 != 2.0):
+        x = np.abs(x) + f32(0.01)
+    if n > 8:
+        x[:7] = [-2, -1, -0.5, 0, 0.5, 1, 2] if kind not in ("log", "sqrt", "pow") else x[:7]
+    xd, od, gd = Dev(x, offset), Dev.empty(n, offset), Dev.empty(n, offset)
+    name = f"seera_hip_{kind}_fwd"
+    if kind == "pow":
+        capi.call(name, xd.ptr, p0, od.ptr, gd.ptr, n)
+    elif kind == "clip":
+        capi.call(name, xd.ptr, p0, p1, od.ptr, gd.ptr, n)
+    else:
+        capi.call(name, xd.ptr, od.ptr, gd.ptr, n)
+    want_o, want_g = T.activation(kind, x, p0, p1)
+    out, grad = od.get(), gd.get()
+    exact_o, exact_g = EXACT.get(kind, (False, False))
+    if exact_o:
+        bit_equal(out, want_o, f"{kind} out")
+    else:
+        assert ulp_diff(out, want_o) <= 4, f"{kind} out: {ulp_diff(out, want_o)} ulp"
+    if exact_g:
+        bit_equal(grad, want_g, f"{kind} grad")
+    else:
+        np.testing.assert_allclose(grad, want_g, rtol=1e-5, atol=1e-6, err_msg=f"{kind} grad")
+
+
+@pytest.mark.parametrize("shape", [(256, 10), (64, 128), (3, 1), (5, 257), (2, 1000), (7, 65),
+                                   (1, 64)])
+def test_softmax_and_vjp(shape):
+    r = np.random.default_rng(shape[0] * 1000 + shape[1])
+    x = (r.standard_normal(shape) * 4).astype(f32)
+    d = r.standard_normal(shape).astype(f32)
+    N, C = shape
+    xd, sd = Dev(x), Dev.empty(shape)
+    capi.call("seera_hip_softmax_fwd", xd.ptr, sd.ptr, N, C)
+    s = sd.get()
+    np.testing.assert_allclose(s, T.softmax(x), rtol=1e-5, atol=1e-7)
+    dd, dxd = Dev(d), Dev.empty(shape)
+    capi.call("seera_hip_softmax_vjp", sd.ptr, dd.ptr, dxd.ptr, N, C)
+    np.testing.assert_allclose(dxd.get(), T.softmax_vjp(s, d), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("op,name", [("add", "elemadd"), ("sub", "elemsub"), ("mul", "elemmult"),
+                                     ("div", "elemdiv")])
+@pytest.mark.parametrize("n", [1, 5, 4096, 100003])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_elementwise(op, name, n, offset):
+    r = np.random.default_rng(n)
+    a = r.standard_normal(n).astype(f32)
+    b = r.standard_normal(n).astype(f32)
+    if n > 4:
+        b[1] = 0.0  # x / 0 = inf, 0 / 0 = nan, both as IEEE
+        a[2] = b[2] = 0.0
+    A, B, C = Dev(a, offset), Dev(b, offset), Dev.empty(n, offset)
+    capi.call(f"seera_hip_{name}", A.ptr, B.ptr, C.ptr, n)
+    bit_equal(C.get(), T.elementwise(op, a, b), name)
+
+
+@pytest.mark.parametrize("op,name,k", [("mul", "scaler_multiply_f", -1.5),
+                                       ("add", "scaler_add_f", 0.25), ("pow", "power_of", 2.0),
+                                       ("pow", "power_of", 0.5)])
+@pytest.mark.parametrize("n", [3, 4096, 10001])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_scalar_inplace(op, name, k, n, offset):
+    r = np.random.default_rng(n)
+    a = np.abs(r.standard_normal(n)).astype(f32) + f32(0.01)
+    A = Dev(a, offset)
+    capi.call(f"seera_hip_{name}", A.ptr, k, n)
+    want = T.scalar_inplace(op, a, k)
+    if op == "pow":
+        assert ulp_diff(A.get(), want) <= 4
+    else:
+        bit_equal(A.get(), want, name)
+
+
+BCAST = [((2, 3, 4, 5), (1, 3, 1, 1)), ((1, 1, 64, 128), (1, 1, 1, 128)),
+         ((2, 1, 4, 1), (1, 3, 1, 5)), ((1, 1, 1, 1), (2, 3, 4, 5)), ((2, 3, 4, 5), (2, 3, 4, 5)),
+         ((16, 64, 56, 56), (1, 64, 1, 1))]
+
+
+@pytest.mark.parametrize("a4,b4", BCAST)
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_broadcast(a4, b4, op):
+    r = np.random.default_rng(sum(a4) + sum(b4))
+    a = r.standard_normal(a4).astype(f32)
+    b = r.standard_normal(b4).astype(f32)
+    o = T.broadcast_shape(a4, b4)
+    A, B, C = Dev(a), Dev(b), Dev.empty(o)
+    capi.call(f"seera_hip_broadcast_{op}_4d", A.ptr, B.ptr, C.ptr, *a4, *b4)
+    bit_equal(C.get(), T.broadcast_4d(op, a, b, a4, b4), f"broadcast {op}")
+
+
+def test_broadcast_mismatch_is_an_error():
+    A, C = Dev(np.zeros(24, f32)), Dev.empty(24)
+    with pytest.raises(capi.SeeraError, match="broadcast"):
+        capi.call("seera_hip_broadcast_add_4d", A.ptr, A.ptr, C.ptr, 2, 3, 4, 1, 1, 2, 1, 1)
+
+
+@pytest.mark.parametrize("shape,sh,sw", [((2, 3, 5, 4), 2, 2), ((1, 2, 7, 3), 1, 3),
+                                         ((4, 8, 14, 14), 3, 2), ((32, 64, 28, 28), 2, 2)])
+def test_unpooling(shape, sh, sw):
+    r = np.random.default_rng(shape[2])
+    x = r.standard_normal(shape).astype(f32)
+    B, C, H, W = shape
+    up = (B, C, H * sh, W * sw)
+    X, O = Dev(x), Dev.empty(up)
+    capi.call("seera_hip_unpooling_fwd", X.ptr, O.ptr, B, C, H, W, sh, sw)
+    bit_equal(O.get(), T.unpool_fwd(x, sh, sw), "unpool fwd")
+    d = r.standard_normal(up).astype(f32)
+    D, DX = Dev(d), Dev.empty(shape)
+    capi.call("seera_hip_unpooling_bwd", D.ptr, DX.ptr, B, C, H, W, sh, sw)
+    bit_equal(DX.get(), T.unpool_bwd(d, sh, sw), "unpool bwd")
+
+
+DIMS = [((4, 5, 6), 0), ((4, 5, 6), 1), ((4, 5, 6), 2), ((64, 128), 0), ((64, 10), 1), ((3,), 0),
+        ((2, 3, 4, 5), 3), ((2, 3, 4, 5), 1), ((256, 512), 0), ((7, 1, 9), 1)]
+
+
+def _red(name, dims, dim, *ptrs):
+    d = np.ascontiguousarray(dims, np.int32)
+    fn = getattr(capi.load(), f"seera_hip_{name}")
+    capi.check(fn(*ptrs, len(dims), dim, d.ctypes.data_as(ctypes.c_void_p)))
+
+
+@pytest.mark.parametrize("dims,dim", DIMS)
+def test_reductions(dims, dim):
+    r = np.random.default_rng(len(dims) * 10 + dim)
+    a = r.standard_normal(dims).astype(f32)
+    if a.size > 8:
+        a.ravel()[3] = a.ravel()[5] = a.max()  # ties for argmax / max backward
+        a.ravel()[4] = a.ravel()[6] = a.min()
+    out_shape = T.reduce_fwd("sum", a, dims, dim).shape
+    A = Dev(a)
+    for kind in ("sum", "mean", "max", "min"):
+        O = Dev.empty(out_shape)
+        _red(f"{kind}_fwd", dims, dim, A.ptr, O.ptr)
+        bit_equal(O.get(), T.reduce_fwd(kind, a, dims, dim), f"{kind} fwd")
+    for kind in ("argmax", "argmin"):
+        O = Dev.empty(out_shape, dtype=np.int32)
+        _red(f"{kind}_fwd", dims, dim, A.ptr, O.ptr)
+        bit_equal(O.get(), T.reduce_fwd(kind, a, dims, dim), f"{kind} fwd")
+    g = r.standard_normal(out_shape).astype(f32)
+    G = Dev(g)
+    for kind in ("sum", "mean"):
+        DA = Dev.empty(dims)
+        _red(f"{kind}_bwd", dims, dim, G.ptr, DA.ptr)
+        bit_equal(DA.get(), T.reduce_bwd(kind, g, dims, dim), f"{kind} bwd")
+    for kind in ("max", "min"):
+        y = T.reduce_fwd(kind, a, dims, dim)
+        Y, DA = Dev(y), Dev.empty(dims)
+        _red(f"{kind}_bwd", dims, dim, G.ptr, A.ptr, Y.ptr, DA.ptr)
+        bit_equal(DA.get(), T.reduce_bwd(kind, g, dims, dim, a, y), f"{kind} bwd")
+
+
+def test_reduction_argument_errors():
+    A, O = Dev(np.zeros(6, f32)), Dev.empty(6)
+    with pytest.raises(capi.SeeraError, match="dim"):
+        _red("sum_fwd", (2, 3), 2, A.ptr, O.ptr)
+    with pytest.raises(capi.SeeraError, match="empty"):
+        _red("max_fwd", (2, 0), 1, A.ptr, O.ptr)
+
+
+# ---- the seera_cuda module the way cuTen.py / Seera_Engine.py drive it ----
+
+@pytest.fixture(scope="module")
+def sc():
+    import ml_framework_amd
+
+    return ml_framework_amd.seera_cuda()
+
+
+def test_cuten_dense_layer_sequence_config1(sc):
+    """BASELINE config 1's Dense layer through the reference's call order:
+    cuda_matmul (cuTen.py:447-449) -> broadcast_add_4d of the bias
+    (cuTen.py:150-160, shapes padded to 4-D) -> cuda_relu_fwd (cuTen.py:329)
+    -> cuda_softmax_fwd (cuTen.py:401); backward cuda_softmax_vjp
+    (Seera_Engine.py:364) -> cuda_elemmult by the ReLU grad -> cuda_sum_fwd
+    over the batch for db (cuTen.py:490, Seera_Engine.py:43-65) ->
+    cuda_matmul_bwd (Seera_Engine.py:539). Inputs: seed 0, X ~ N(0, 1)
+    [64, 784], W Kaiming-uniform(fan_in 784) [784, 128], b = 0,
+    dY ~ N(0, 1) [64, 128]."""
+    r = np.random.default_rng(0)
+    M, K, N = 64, 784, 128
+    x = r.standard_normal((M, K)).astype(f32)
+    lim = np.sqrt(6.0 / K)
+    w = r.uniform(-lim, lim, (K, N)).astype(f32)
+    b = np.zeros(N, f32)
+    dy = r.standard_normal((M, N)).astype(f32)
+    px, pw, pb, pdy = (sc.to_device_f32(v) for v in (x, w, b, dy))
+    py = sc.cuda_malloc_f32(M * N)
+    sc.cuda_matmul(px, pw, py, M, N, K, 1)
+    y = sc.to_host_f32(py, (M, N))
+    assert_parity(y, S.matmul(fp16r(x), fp16r(w)), "cfg1 Y")
+    pz = sc.cuda_malloc_f32(M * N)
+    sc.broadcast_add_4d(py, pb, pz, 1, 1, M, N, 1, 1, 1, N)
+    z = sc.to_host_f32(pz, (M, N))
+    bit_equal(z, T.broadcast_4d("add", y, b, (1, 1, M, N), (1, 1, 1, N)).reshape(M, N), "bias")
+    pa, pg = sc.cuda_malloc_f32(M * N), sc.cuda_malloc_f32(M * N)
+    sc.cuda_relu_fwd(pz, pa, pg, M * N)
+    a, g = sc.to_host_f32(pa, (M, N)), sc.to_host_f32(pg, (M, N))
+    wa, wg = T.activation("relu", z)
+    bit_equal(a, wa, "relu out")
+    bit_equal(g, wg, "relu grad")
+    ps = sc.cuda_malloc_f32(M * N)
+    sc.cuda_softmax_fwd(pa, ps, M, N)
+    s = sc.to_host_f32(ps, (M, N))
+    np.testing.assert_allclose(s, T.softmax(a), rtol=1e-5, atol=1e-7)
+    # backward
+    pds = sc.cuda_malloc_f32(M * N)
+    sc.cuda_softmax_vjp(ps, pdy, pds, M, N)
+    ds = sc.to_host_f32(pds, (M, N))
+    np.testing.assert_allclose(ds, T.softmax_vjp(s, dy), rtol=1e-5, atol=1e-6)
+    pdz = sc.cuda_malloc_f32(M * N)
+    sc.cuda_elemmult(pds, pg, pdz, M * N)
+    dz = sc.to_host_f32(pdz, (M, N))
+    bit_equal(dz, ds * g, "relu backward")
+    pdb = sc.cuda_malloc_f32(N)
+    sc.cuda_sum_fwd(pdz, pdb, 2, 0, np.array([M, N], np.int32))
+    bit_equal(sc.to_host_f32(pdb, (N,)), T.reduce_fwd("sum", dz, (M, N), 0), "db")
+    np.testing.assert_allclose(sc.to_host_f32(pdb, (N,)), dz.astype(np.float64).sum(0),
+                               rtol=1e-5, atol=1e-5)
+    pdx, pdw = sc.cuda_malloc_f32(M * K), sc.cuda_malloc_f32(K * N)
+    sc.cuda_matmul_bwd(px, pw, pdz, pdx, pdw, M, N, K, 1)
+    rdx, rdw = S.matmul_bwd(fp16r(x), fp16r(w), fp16r(dz))
+    assert_parity(sc.to_host_f32(pdx, (M, K)), rdx, "cfg1 dX")
+    assert_parity(sc.to_host_f32(pdw, (K, N)), rdw, "cfg1 dW")
+    for p in (px, pw, pb, pdy, py, pz, pa, pg, ps, pds, pdz, pdb, pdx, pdw):
+        sc.cuda_free(p)
+
+
+def test_module_reductions_unpool_and_scalars(sc):
+    """cuTen's sum / mean / max / min (cuTen.py:487-534), unpool
+    (cuTen.py:613-630), scalar add / multiply / power on a copy
+    (cuTen.py:166-222) and the activation family through the module."""
+    r = np.random.default_rng(11)
+    a = r.standard_normal((3, 4, 5)).astype(f32)
+    pa = sc.to_device_f32(a)
+    dims = np.array(a.shape, np.int32)
+    for name in ("sum", "mean", "max", "min"):
+        po = sc.cuda_malloc_f32(3 * 5)
+        getattr(sc, f"cuda_{name}_fwd")(pa, po, 3, 1, dims)
+        bit_equal(sc.to_host_f32(po, (3, 5)), T.reduce_fwd(name, a, a.shape, 1), name)
+        sc.cuda_free(po)
+    pi = sc.cuda_malloc_i32(3 * 5)
+    sc.cuda_argmax_fwd(pa, pi, 3, 1, dims)
+    bit_equal(sc.to_host_i32(pi, (3, 5)), T.reduce_fwd("argmax", a, a.shape, 1), "argmax")
+    x4 = r.standard_normal((2, 3, 4, 4)).astype(f32)
+    px = sc.to_device_f32(x4)
+    pu = sc.cuda_malloc_f32(2 * 3 * 8 * 8)
+    sc.cuda_unpooling_fwd(px, pu, 2, 3, 4, 4, 2, 2)
+    bit_equal(sc.to_host_f32(pu, (2, 3, 8, 8)), T.unpool_fwd(x4, 2, 2), "unpool")
+    pc = sc.cuda_malloc_f32(a.size)
+    sc.cuda_memcopy_devicetodevice(pc, pa, a.size)
+    sc.cuda_scaler_add_f(pc, 1.5, a.size)
+    sc.cuda_scaler_multiply_f(pc, -2.0, a.size)
+    bit_equal(sc.to_host_f32(pc, a.shape), (a + f32(1.5)) * f32(-2.0), "scalar add, multiply")
+    sc.cuda_power_of(pc, 2.0, a.size)
+    assert ulp_diff(sc.to_host_f32(pc, a.shape), ((a + f32(1.5)) * f32(-2.0)) ** f32(2.0)) <= 4
+    po, pg = sc.cuda_malloc_f32(a.size), sc.cuda_malloc_f32(a.size)
+    sc.cuda_clip_fwd(pa, -0.5, 0.5, po, pg, a.size)
+    bit_equal(sc.to_host_f32(po, a.shape), T.activation("clip", a, -0.5, 0.5)[0], "clip")
+    sc.cuda_pow_fwd(pa, 2.0, po, pg, a.size)
+    assert ulp_diff(sc.to_host_f32(po, a.shape), T.activation("pow", a, 2.0)[0]) <= 4
+    for p in (pa, pi, px, pu, pc, po, pg):
+        sc.cuda_free(p)
