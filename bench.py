@@ -100,14 +100,41 @@ def bench_gemm(n, steps, warmup, stream, with_bwd):
     return res
 
 
+_INPUTS = {}
+
+
+def conv_inputs():
+    """Config 4's seeded inputs: X ~ N(0,1) [128,64,56,56], W Kaiming-uniform
+    (fan_in 576) [64,64,3,3], dY ~ N(0,1); all fp16-rounded."""
+    if "conv" not in _INPUTS:
+        r = np.random.default_rng(0)
+        x = fp16r(r.standard_normal((128, 64, 56, 56)))
+        lim = np.sqrt(6 / 576)
+        w = fp16r(r.uniform(-lim, lim, (64, 64, 3, 3)))
+        dy = fp16r(r.standard_normal((128, 64, 56, 56)))
+        _INPUTS["conv"] = {"x": x, "w": w, "dy": dy, "rng": r}
+    return _INPUTS["conv"]
+
+
+def convT_inputs():
+    """Config 5's seeded inputs: X ~ N(0,1) [32,128,28,28], W Kaiming-uniform
+    (fan_in 2048) [128,64,4,4], dY ~ N(0,1) [32,64,56,56]; fp16-rounded."""
+    if "convT" not in _INPUTS:
+        r = np.random.default_rng(0)
+        x = fp16r(r.standard_normal((32, 128, 28, 28)))
+        lim = np.sqrt(6 / 2048)
+        w = fp16r(r.uniform(-lim, lim, (128, 64, 4, 4)))
+        dy = fp16r(r.standard_normal((32, 64, 56, 56)))
+        _INPUTS["convT"] = {"x": x, "w": w, "dy": dy}
+    return _INPUTS["convT"]
+
+
 def bench_conv(steps, warmup, stream):
     """Config 4: Conv2D 3x3 s1 p1, N=128, 64->64, 56x56; fwd + (dX, dW)."""
-    r = np.random.default_rng(0)
+    cv = conv_inputs()
+    r = np.random.default_rng(1)
     N, C, H, W, F = 128, 64, 56, 56, 64
-    x = fp16r(r.standard_normal((N, C, H, W)))
-    lim = np.sqrt(6 / 576)
-    w = fp16r(r.uniform(-lim, lim, (F, C, 3, 3)))
-    dy = fp16r(r.standard_normal((N, F, H, W)))
+    x, w, dy = cv["x"], cv["w"], cv["dy"]
     lib = capi.load()
     px, pw, pdy = (DeviceBuffer.from_array(v) for v in (x, w, dy))
     py, pdx, pdw = DeviceBuffer(x.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(w.nbytes)
@@ -143,12 +170,9 @@ def bench_conv(steps, warmup, stream):
 
 def bench_convT(steps, warmup, stream):
     """Config 5: ConvTranspose2D 4x4 s2 p1, N=32, 128->64, 28x28 -> 56x56."""
-    r = np.random.default_rng(0)
+    ct = convT_inputs()
     N, Cin, H, W, Cout = 32, 128, 28, 28, 64
-    x = fp16r(r.standard_normal((N, Cin, H, W)))
-    lim = np.sqrt(6 / 2048)
-    w = fp16r(r.uniform(-lim, lim, (Cin, Cout, 4, 4)))
-    dy = fp16r(r.standard_normal((N, Cout, 56, 56)))
+    x, w, dy = ct["x"], ct["w"], ct["dy"]
     lib = capi.load()
     px, pw, pdy = (DeviceBuffer.from_array(v) for v in (x, w, dy))
     py, pdx, pdw = DeviceBuffer(dy.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(w.nbytes)
@@ -388,24 +412,34 @@ def bench_alloc(reps=50):
             "mlp_step_sync_alloc_ms_uncached": round(ms_uncached, 4)}
 
 
+def _median_seconds(fn, reps):
+    fn()  # warm-up
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
 def cpu_baseline(n=4096, reps=5):
-    """The oracle's seera_cpp restatement (OpenBLAS sgemm) on this host."""
+    """The oracle's seera_cpp restatement on this host's cores: the 4096^3
+    sgemm (tensor_ops.cpp:9-15) for the GEMM half of the metric, and the
+    Conv2D / ConvTranspose2D forward + backward (conv_ops.cpp:95-287: im2col,
+    per-sample sgemm in an OpenMP loop over the batch, col2im) for the conv
+    half, on the same seeded fp16-rounded inputs as the GPU legs. The conv
+    legs run on a bounded sample (a slice of the batch; the rate is per
+    FLOP, so the sample's TFLOP/s stands for the whole batch)."""
     import oracle
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     oracle.load(threads)
+    S = oracle.seera_cpp
     r = np.random.default_rng(n)
     a = fp16r(r.uniform(-1, 1, (n, n)))
     b = fp16r(r.uniform(-1, 1, (n, n)))
-    S = oracle.seera_cpp
-    S.matmul(a, b)
-    ts = []
-    for _ in range(reps):
-        t = time.perf_counter()
-        S.matmul(a, b)
-        ts.append(time.perf_counter() - t)
-    sec = float(np.median(ts))
-    return {
+    sec = _median_seconds(lambda: S.matmul(a, b), reps)
+    out = {
         "value": round(2 * n ** 3 / sec / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
@@ -413,6 +447,31 @@ def cpu_baseline(n=4096, reps=5):
         "sample": f"{n}^3 fp32 GEMM (oracle_matmul over {oracle.backend()}), "
                   f"median of {reps} after 1 warm-up",
     }
+    # Config 4 (Conv2D 3x3 s1 p1, 64 -> 64, 56x56): first 16 of the 128 images.
+    cv = conv_inputs()
+    nb = 16
+    x, w, dy = cv["x"][:nb], cv["w"], cv["dy"][:nb]
+    t_f = _median_seconds(lambda: S.conv2d_forward(x, w, 1, 1, 1, 1), reps)
+    t_b = _median_seconds(lambda: S.conv2d_backward(dy, x, w, 1, 1, 1, 1), reps)
+    fl = 2.0 * nb * 64 * 56 * 56 * 64 * 9
+    out["conv2d_cfg4"] = {
+        "value": round(3 * fl / (t_f + t_b) / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+        "kind": "port", "ms_fwd": round(t_f * 1e3, 2), "ms_bwd": round(t_b * 1e3, 2),
+        "sample": f"Conv2D fwd + bwd (dX, dW) of images 0-{nb - 1} of config 4's batch of 128 "
+                  f"(oracle_conv2d_forward/backward), median of {reps} after 1 warm-up"}
+    # Config 5 (ConvTranspose2D 4x4 s2 p1, 128 -> 64, 28 -> 56): 8 of 32 images.
+    ct = convT_inputs()
+    nb = 8
+    x, w, dy = ct["x"][:nb], ct["w"], ct["dy"][:nb]
+    t_f = _median_seconds(lambda: S.conv_transpose2d_forward(x, w, 2, 2, 1, 1), reps)
+    t_b = _median_seconds(lambda: S.conv_transpose2d_backward(dy, x, w, 2, 2, 1, 1), reps)
+    fl = 2.0 * nb * 128 * 28 * 28 * 64 * 16
+    out["convT_cfg5"] = {
+        "value": round(3 * fl / (t_f + t_b) / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+        "kind": "port", "ms_fwd": round(t_f * 1e3, 2), "ms_bwd": round(t_b * 1e3, 2),
+        "sample": f"ConvTranspose2D fwd + bwd of images 0-{nb - 1} of config 5's batch of 32 "
+                  f"(oracle_conv_transpose2d_forward/backward), median of {reps} after 1 warm-up"}
+    return out
 
 
 def copy_calibration(nbytes, reps=3):
@@ -438,6 +497,37 @@ def traffic_from_profiles():
         except (OSError, ValueError):
             return None
     return None
+
+
+# Algorithmic HBM bytes of one forward + backward, counted at the API: each
+# call reads its inputs once and writes its outputs once (fp32), nothing else.
+#   Conv2D config 4: fwd X, W -> Y; bwd W, X, dY -> dX, dW.
+_X4, _W4 = 128 * 64 * 56 * 56 * 4, 64 * 64 * 9 * 4
+CFG4_BYTES = (_X4 + _W4 + _X4) + (_W4 + _X4 + _X4 + _X4 + _W4)
+#   ConvTranspose2D config 5: fwd X, W -> Y; bwd W, X, dY -> dX, dW.
+_X5, _Y5, _W5 = 32 * 128 * 28 * 28 * 4, 32 * 64 * 56 * 56 * 4, 128 * 64 * 16 * 4
+CFG5_BYTES = (_X5 + _W5 + _Y5) + (_W5 + _X5 + _Y5 + _X5 + _W5)
+
+
+def conv_roofline(name, flops, nbytes, ms):
+    """HBM roofline of a convolution's forward + backward: achieved GB/s over
+    the algorithmic bytes against 8 TB/s, with the TFLOP/s those bytes allow
+    (AI x 8 TB/s) beside the achieved TFLOP/s."""
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    ai = flops / nbytes
+    traffic = None
+    path = os.path.join(PROFILES, f"{name}_traffic.json")
+    if os.path.exists(path):
+        try:
+            traffic = json.load(open(path)).get("bytes_per_fwd_bwd")
+        except (OSError, ValueError):
+            traffic = None
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes": nbytes, "flop": flops,
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "roof_tflops": round(ai * PEAK_HBM_GBS * 1e9 / 1e12, 1),
+            "roof_pct_mfma_peak": round(100 * ai * PEAK_HBM_GBS * 1e9 / 1e12 / PEAK_FP16_TFLOPS, 1)}
 
 
 def main():
@@ -508,8 +598,10 @@ def main():
                              "fwd_bwd_tflops": round(3 * f / (gm["ms_fwd_bwd"] * 1e-3) / 1e12, 2)}
         extras["gemm_sweep_cfg2"] = sweep
         cv = bench_conv(20, 3, stream)
-        conv_flops = 29.6e9 * 3  # 2*N*F*Ho*Wo*C*R*S per pass, 3 passes
+        conv_flops = 3 * 2.0 * 128 * 64 * 56 * 56 * 64 * 9  # 2*N*F*Ho*Wo*C*R*S per pass, 3 passes
         extras["conv2d_cfg4"] = {
+            "roofline": conv_roofline("conv2d_cfg4", conv_flops, CFG4_BYTES,
+                                      cv["ms_fwd"] + cv["ms_bwd"]),
             "ms_fwd": round(cv["ms_fwd"], 4), "ms_bwd": round(cv["ms_bwd"], 4),
             "ms_fwd_fused_bias_relu": round(cv["ms_fwd_fused_bias_relu"], 4),
             "ms_bias_grad": round(cv["ms_bias_grad"], 4),
@@ -522,8 +614,10 @@ def main():
                                    / 1e12 / PEAK_FP16_TFLOPS, 2),
         }
         ct = bench_convT(20, 3, stream)
-        ct_flops = 6.58e9 * 3
+        ct_flops = 3 * 2.0 * 32 * 128 * 28 * 28 * 64 * 16
         extras["convT_cfg5"] = {
+            "roofline": conv_roofline("convT_cfg5", ct_flops, CFG5_BYTES,
+                                      ct["ms_fwd"] + ct["ms_bwd"]),
             "ms_fwd": round(ct["ms_fwd"], 4), "ms_bwd": round(ct["ms_bwd"], 4),
             "fwd_bwd_tflops": round(ct_flops / ((ct["ms_fwd"] + ct["ms_bwd"]) * 1e-3) / 1e12, 2),
         }
