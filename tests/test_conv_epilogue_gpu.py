@@ -107,3 +107,29 @@ def test_conv_bias_grad_empty_batch_is_zero():
         pb.fill(0x7F)
         capi.call("seera_hip_conv_bias_grad", None, pb.ptr, 0, 4, 9)
         assert np.array_equal(pb.to_array((4,)), np.zeros(4, np.float32))
+
+
+@pytest.mark.parametrize("case", SHAPES, ids=[c[0] for c in SHAPES])
+@pytest.mark.parametrize("act", [capi.SEERA_ACT_NONE, capi.SEERA_ACT_RELU])
+def test_fused_conv_against_oracle(case, act):
+    """The fused Conv2D-layer forward against the oracle directly: the
+    seera_cpp restatement's conv2d_forward on fp16-rounded operands
+    (conv_ops.cpp:95-122), then + bias and ReLU in fp32, at the north-star
+    tolerance; the mask against the oracle's sign where it is clear of 0."""
+    import oracle
+    from oracle import fp16r
+    from tests.helpers import assert_parity
+
+    _, N, C, H, W, F, K, s, p = case
+    r = np.random.default_rng(N * 7 + C + F + K + act)
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (r.standard_normal((F, C, K, K)) * 0.2).astype(np.float32)
+    bias = r.uniform(-0.5, 0.5, F).astype(np.float32)
+    got, mask = _fused(x, w, bias, s, p, act)
+    pre = oracle.seera_cpp.conv2d_forward(fp16r(x), fp16r(w), s, s, p, p) + \
+        bias[None, :, None, None]
+    want = np.where(pre > 0, pre, np.float32(0)) if act == capi.SEERA_ACT_RELU else pre
+    assert_parity(got, want, f"fused conv {case[0]}")
+    if act == capi.SEERA_ACT_RELU:
+        clear = np.abs(pre) > 1e-4 * np.sqrt(C * K * K)
+        assert np.array_equal(mask[clear], (pre[clear] > 0).astype(np.float32))

@@ -138,3 +138,99 @@ def test_fused_relu_backward_equals_unfused(M, K, N, nb):
         got = pda2.to_array(a.shape)
         assert np.array_equal(_bits(got), _bits(want))
         assert np.array_equal(pdb2.to_array(b.shape), pdb.to_array(b.shape))
+
+
+def _oracle_epilogue(pre, act):
+    return np.where(pre > 0, pre, np.float32(0)) if act == capi.SEERA_ACT_RELU else pre
+
+
+def _mask_agrees(mask, pre_ref, scale):
+    """The mask must equal (pre > 0) of the oracle wherever the oracle's
+    pre-activation is clear of 0 by more than the parity tolerance (the two
+    sums differ in order, so values within rounding of 0 may fall either way)."""
+    clear = np.abs(pre_ref) > 1e-4 * scale
+    return np.array_equal(mask[clear], (pre_ref[clear] > 0).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,K,N,nb", [s for s in SHAPES if s[1] > 0])
+@pytest.mark.parametrize("act", [capi.SEERA_ACT_NONE, capi.SEERA_ACT_RELU])
+def test_fused_bias_act_against_oracle(M, K, N, nb, act):
+    """The fused Dense forward against the oracle directly: the seera_cpp
+    restatement's matmul on fp16-rounded operands (tensor_ops.cpp:9-15), then
+    the bias add and ReLU in fp32 (broadcast.cu:12-64, activations.cu:9-15),
+    at the north-star tolerance; the ReLU mask against the oracle's sign."""
+    import oracle
+    from oracle import fp16r
+
+    r = np.random.default_rng(M * 13 + K + N + act)
+    a = r.uniform(-1, 1, (nb, M, K)).astype(np.float32)
+    b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = r.uniform(-1, 1, N).astype(np.float32)
+    lib = load()
+    with DeviceBuffer.from_array(a) as A, DeviceBuffer.from_array(b) as B, \
+            DeviceBuffer.from_array(bias) as Bi, DeviceBuffer(nb * M * N * 4) as C, \
+            DeviceBuffer(nb * M * N * 4) as Mk:
+        check(lib.seera_hip_matmul_bias_act(A.ptr, B.ptr, Bi.ptr, C.ptr, Mk.ptr, M, N, K, nb, act))
+        got, mask = C.to_array((nb, M, N)), Mk.to_array((nb, M, N))
+    pre = oracle.seera_cpp.matmul_batched(fp16r(a), fp16r(b)) + bias
+    assert_parity(got, _oracle_epilogue(pre, act), f"fused fwd {M}x{K}x{N}x{nb}")
+    if act == capi.SEERA_ACT_RELU:
+        assert _mask_agrees(mask, pre, np.sqrt(K))
+
+
+@pytest.mark.parametrize("M,K,N,nb", [s for s in BWD_SHAPES if s[1] > 0])
+def test_fused_relu_backward_against_oracle(M, K, N, nb):
+    """dA = (dC . B^T) * mask and dB = A^T . dC against the oracle's GEMM
+    backward on fp16-rounded operands (Seera_Engine.py:557-564) times the
+    mask (Seera_Engine.py:575-583), at the north-star tolerance."""
+    import oracle
+    from oracle import fp16r
+
+    r = np.random.default_rng(M * 7 + K + N)
+    a = np.maximum(r.standard_normal((nb, M, K)), 0).astype(np.float32)
+    b = r.standard_normal((K, N)).astype(np.float32)
+    dc = r.standard_normal((nb, M, N)).astype(np.float32)
+    mask = (r.uniform(0, 1, (nb, M, K)) > 0.4).astype(np.float32)
+    with DeviceBuffer.from_array(a) as pa, DeviceBuffer.from_array(b) as pb, \
+            DeviceBuffer.from_array(dc) as pdc, DeviceBuffer.from_array(mask) as pm, \
+            DeviceBuffer(a.nbytes) as pda, DeviceBuffer(b.nbytes) as pdb:
+        capi.call("seera_hip_matmul_bwd_relu", pa.ptr, pb.ptr, pdc.ptr, pm.ptr, pda.ptr, pdb.ptr,
+                  M, N, K, nb)
+        da, db = pda.to_array(a.shape), pdb.to_array(b.shape)
+    rda, rdb = oracle.seera_cpp.matmul_bwd(fp16r(a), fp16r(b), fp16r(dc))
+    assert_parity(da, rda * mask, "fused dA")
+    assert_parity(db, rdb, "dB")
+
+
+def test_config1_dense_on_its_own_inputs():
+    """BASELINE config 1 on the GPU with its own inputs (seed 0: X ~ N(0,1)
+    [64, 784], W Kaiming-uniform(fan_in 784) [784, 128], b = 0, dY ~ N(0,1)
+    [64, 128]): the fused forward, the GEMM backward and db = sum of dY over
+    the batch, each against the oracle (db against an fp64 sum)."""
+    import oracle
+    from oracle import fp16r
+
+    r = np.random.default_rng(0)
+    M, K, N = 64, 784, 128
+    x = r.standard_normal((M, K)).astype(np.float32)
+    lim = np.sqrt(6.0 / K)
+    w = r.uniform(-lim, lim, (K, N)).astype(np.float32)
+    bias = np.zeros(N, np.float32)
+    dy = r.standard_normal((M, N)).astype(np.float32)
+    S = oracle.seera_cpp
+    lib = load()
+    with DeviceBuffer.from_array(x) as px, DeviceBuffer.from_array(w) as pw, \
+            DeviceBuffer.from_array(bias) as pb, DeviceBuffer.from_array(dy) as pdy, \
+            DeviceBuffer(M * N * 4) as py, DeviceBuffer(M * K * 4) as pdx, \
+            DeviceBuffer(K * N * 4) as pdw, DeviceBuffer(N * 4) as pdb:
+        check(lib.seera_hip_matmul_bias_act(px.ptr, pw.ptr, pb.ptr, py.ptr, None, M, N, K, 1,
+                                            capi.SEERA_ACT_NONE))
+        check(lib.seera_hip_matmul_bwd(px.ptr, pw.ptr, pdy.ptr, pdx.ptr, pdw.ptr, M, N, K, 1))
+        check(lib.seera_hip_bias_grad(pdy.ptr, pdb.ptr, M, N))
+        y, dx, dw, db = (py.to_array((M, N)), pdx.to_array((M, K)), pdw.to_array((K, N)),
+                         pdb.to_array((N,)))
+    assert_parity(y, S.matmul(fp16r(x), fp16r(w)) + bias, "cfg1 Y")
+    rdx, rdw = S.matmul_bwd(fp16r(x), fp16r(w), fp16r(dy))
+    assert_parity(dx, rdx, "cfg1 dX")
+    assert_parity(dw, rdw, "cfg1 dW")
+    assert_parity(db, dy.astype(np.float64).sum(axis=0), "cfg1 db", rel=1e-6, mabs=1e-4)
