@@ -390,7 +390,9 @@ int seera_hip_stream_synchronize(void *stream);
  *     destroyed, so eager calls of any size may run between replays;
  *   - a replay and an eager call queued on the capture stream itself are
  *     ordered; a replay on another stream must not overlap eager calls on the
- *     capture stream (they share that stream's workspace).
+ *     capture stream (they share that stream's workspace);
+ *   - seera_hip_stream_destroy frees the stream's workspace (or keeps it
+ *     while a graph is live on the device).
  * The _async entry points clear memory with kernels, not memset nodes. */
 int seera_hip_graph_capture_begin(void *stream);
 int seera_hip_graph_capture_end(void *stream, void **graph_exec);

@@ -547,7 +547,9 @@ int seera_hip_stream_create(void** stream) {
 }
 int seera_hip_stream_destroy(void* stream) {
     return guarded([&] {
-        if (stream) SEERA_HIP_TRY(hipStreamDestroy(as_stream(stream)));
+        if (!stream) return (int)SEERA_OK;
+        SEERA_TRY(stream_destroyed(as_stream(stream)));  // its workspace goes with it
+        SEERA_HIP_TRY(hipStreamDestroy(as_stream(stream)));
         return (int)SEERA_OK;
     });
 }

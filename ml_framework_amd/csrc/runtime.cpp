@@ -109,6 +109,14 @@ int workspace(size_t bytes, void** out, hipStream_t st) {
     return e;
 }
 
+int stream_destroyed(hipStream_t st) {
+    if (!st) return SEERA_OK;
+    int dev = 0;
+    SEERA_HIP_TRY(hipStreamGetDevice(st, &dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_pool.stream_destroyed(dev, st);
+}
+
 int graph_created(void* exec) {
     int dev = 0;
     SEERA_HIP_TRY(hipGetDevice(&dev));

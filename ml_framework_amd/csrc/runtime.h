@@ -47,6 +47,9 @@ public:
     FixedWorkspace& operator=(const FixedWorkspace&) = delete;
 };
 
+// Called before a stream is destroyed: frees its workspace (or keeps it for
+// the device's live graphs).
+int stream_destroyed(hipStream_t st);
 // Graph bookkeeping for the workspace rule above (capi.cpp calls these when
 // an executable graph is instantiated and destroyed).
 int graph_created(void* exec);

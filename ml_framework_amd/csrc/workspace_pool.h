@@ -12,7 +12,10 @@
 //     address it was captured with; the device's retired buffers are freed
 //     when its last graph is destroyed;
 //   * growing while the stream is being captured is refused (kGrowUnderCapture):
-//     the capture would record a buffer that a later call could free.
+//     the capture would record a buffer that a later call could free;
+//   * destroying a stream frees its workspace (retired instead while a graph
+//     is live on the device), so a new stream that gets the same handle
+//     starts empty.
 //
 // Backend interface (all return 0 on success or a nonzero status):
 //   int alloc(int dev, size_t bytes, void** out);
@@ -63,6 +66,25 @@ public:
         }
         *out = s.ptr;
         return 0;
+    }
+
+    // The stream is being destroyed: its workspace is freed (after a device
+    // synchronize), or retired while a graph on the device may reference it.
+    int stream_destroyed(int dev, const void* stream) {
+        auto it = bufs_.find({dev, stream});
+        if (it == bufs_.end()) return 0;
+        void* p = it->second.ptr;
+        bufs_.erase(it);
+        if (!p) return 0;
+        if (live_graphs_[dev] > 0) {
+            retired_[dev].push_back(p);
+            return 0;
+        }
+        if (int e = b_.sync(dev)) {
+            retired_[dev].push_back(p);  // freed with the device's graphs, or never
+            return e;
+        }
+        return b_.release(dev, p);
     }
 
     void graph_created(const void* exec, int dev) {

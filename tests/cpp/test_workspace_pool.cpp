@@ -143,6 +143,24 @@ void failed_alloc_leaves_clean_state() {
     CHECK(pool.held_bytes() == 4 * MiB);
 }
 
+void stream_destroy_frees_or_retires() {
+    FakeBackend b;
+    Pool pool(b);
+    void *p = nullptr, *q = nullptr, *r = nullptr;
+    CHECK(pool.get(0, kS1, 3 * MiB, false, &p) == 0);
+    CHECK(pool.stream_destroyed(0, kS1) == 0);
+    CHECK(!b.live.count(p) && pool.held_bytes() == 0);
+    CHECK(pool.get(0, kS1, 10, false, &q) == 0);   // a new stream, same handle: fresh
+    CHECK(pool.held_bytes() == MiB);
+    pool.graph_created(kG1, 0);
+    CHECK(pool.stream_destroyed(0, kS1) == 0);
+    CHECK(b.live.count(q) && pool.retired_count() == 1);  // the graph may use it
+    CHECK(pool.stream_destroyed(0, kS2) == 0);            // never used: no-op
+    CHECK(pool.graph_destroyed(kG1) == 0);
+    CHECK(!b.live.count(q) && pool.retired_count() == 0);
+    CHECK(pool.get(0, kS2, 10, false, &r) == 0 && r != nullptr);
+}
+
 }  // namespace
 
 int main() {
@@ -152,6 +170,7 @@ int main() {
     graph_on_other_device_does_not_pin();
     capture_refuses_growth();
     failed_alloc_leaves_clean_state();
+    stream_destroy_frees_or_retires();
     if (g_failures) {
         fprintf(stderr, "%d check(s) failed\n", g_failures);
         return 1;

@@ -37,8 +37,9 @@ class Dev:
     16-byte-aligned allocation (offset 1 exercises the scalar paths)."""
 
     def __init__(self, a, offset=0, dtype=f32):
+        shape = np.shape(a)  # kept as given: ascontiguousarray makes 0-d arrays 1-d
         a = np.ascontiguousarray(a, dtype)
-        self.shape, self.dtype, self.n = a.shape, dtype, a.size
+        self.shape, self.dtype, self.n = shape, dtype, a.size
         self.buf = DeviceBuffer((a.size + offset + 1) * 4)
         self.ptr = self.buf.ptr + 4 * offset
         if a.size:
