@@ -76,6 +76,20 @@ int seera_hip_matmul(const float *A, const float *B, float *C, int M, int N,
 int seera_hip_matmul_async(const float *A, const float *B, float *C, int M,
                            int N, int K, int Nbatch, void *stream);
 
+/* No counterpart in the reference: seera_hip_matmul_async for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). It calls no hipMalloc / hipFree:
+ * its split-K partial sums go to a fixed 8 MiB device array that the
+ * library keeps on each GPU it runs on until the process ends (no shape needs
+ * more than 6.3 MB of partials today; a call that would exceed 8 MiB fails
+ * with SEERA_ERR_INVALID_ARGUMENT). The first call on each device looks up
+ * the array's device address (hipGetSymbolAddress): make it outside graph
+ * capture; later calls need no warm-up. Every
+ * call on one GPU shares that array, so calls that overlap on one GPU (on two
+ * streams, or from two host threads) race: queue them on one stream. */
+int seera_hip_matmul_noalloc(const float *A, const float *B, float *C, int M,
+                             int N, int K, int Nbatch, void *stream);
+
 /* cuda_matmul_bwd (GEMM.cu:164-225; binding cuda_bindings.cpp:267-273).
  * dA[b] = dC[b] . B^T  and  dB = sum_b A[b]^T . dC[b]; both overwritten. */
 int seera_hip_matmul_bwd(const float *A, const float *B, const float *dC,

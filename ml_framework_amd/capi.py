@@ -41,6 +41,7 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_synchronize": ([], _i),
     "seera_hip_matmul": ([_vp, _vp, _vp, _i, _i, _i, _i], _i),
     "seera_hip_matmul_async": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "seera_hip_matmul_noalloc": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
     "seera_hip_matmul_bias_act": ([_vp] * 5 + [_i] * 5, _i),
     "seera_hip_matmul_bias_act_async": ([_vp] * 5 + [_i] * 5 + [_vp], _i),
     "seera_hip_bias_grad": ([_vp, _vp, _i, _i], _i),
