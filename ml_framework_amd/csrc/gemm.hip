@@ -43,6 +43,7 @@ struct GemmProblem {
     float* mask;           // EPI, act == kActRelu: [M, ldc] or nullptr
     int act;               // EPI: kActNone or kActRelu
     static constexpr bool kEpi = EPI;
+    static constexpr bool kPipe = true;  // StageKC / StageMNC load without branches
 
     template <int R, int BK, int NT>
     using SA = typename Operand<A_KC, VA>::template Stager<R, BK, NT>;

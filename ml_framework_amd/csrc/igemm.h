@@ -121,6 +121,114 @@ hipError_t launch_igemm(const P& p, int splits, hipStream_t stream) {
 
 
 // ---------------------------------------------------------------------------
+// Pipelined variant of igemm_kernel for problems with plain (branch-free)
+// stagers: D register sets keep the loads of D K slices in flight instead of
+// one. With one slice in flight every slice costs a full memory round trip
+// (about 1.5 k cycles), which is what bounds the small tiles: a 64x64x32
+// slice is 64 MFMA cycles. Slice s lives in set s % D; iteration kt runs the
+// MFMAs of slice kt from LDS stage kt&1, rounds slice kt+1 from its set into
+// the other stage and at once refills that set with slice kt+1+D. Loads past
+// the last slice re-read it (never stored), so every iteration issues the
+// same loads and the compiler's vmcnt waits stay exact.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WM, int WN, int D, class P>
+__global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
+    using Cfg = TileCfg<BM, BN, BK, WM, WN>;
+    constexpr int NT = Cfg::NT, TM = Cfg::TM, TN = Cfg::TN;
+    static_assert(D >= 2 && D % 2 == 0, "an even number of sets keeps the LDS stage of j fixed");
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    constexpr int STAGE = (BM + BN) * BK;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, p.tiles_n, p.gm, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = blockIdx.z * p.k_split;
+    const int kend = min(p.K, kbeg + p.k_split);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    if (nk > 0) {
+        typename P::template SA<BM, BK, NT> sa[D];
+        typename P::template SB<BN, BK, NT> sb[D];
+        auto kof = [&](int s) { return kbeg + min(s, nk - 1) * BK; };
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            p.init_a(sa[d], m0, tid);
+            p.init_b(sb[d], n0, tid);
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            p.load_a(sa[d], m0, kof(d), kend, tid);
+            p.load_b(sb[d], n0, kof(d), kend, tid);
+        }
+        sa[0].store(smem, tid);
+        sb[0].store(smem + BM * BK, tid);
+        p.load_a(sa[0], m0, kof(D), kend, tid);
+        p.load_b(sb[0], n0, kof(D), kend, tid);
+        __syncthreads();
+        // Whole groups of D iterations, every store and load unconditional
+        // (the MFMAs of iterations past the last slice are skipped): the loop
+        // has one entry state, which keeps the waits exact across its back
+        // edge.
+        for (int kb = 0; kb < nk; kb += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const int kt = kb + j;  // kb is a multiple of D (even): kt & 1 == j & 1
+                const half_t* const now = smem + (j & 1) * STAGE;
+                half_t* const next = smem + ((j + 1) & 1) * STAGE;
+                if (kt < nk) mfma_slice<BK, TM, TN>(now, now + BM * BK, wm0, wn0, lane, acc);
+                sa[(j + 1) % D].store(next, tid);
+                sb[(j + 1) % D].store(next + BM * BK, tid);
+                p.load_a(sa[(j + 1) % D], m0, kof(kt + 1 + D), kend, tid);
+                p.load_b(sb[(j + 1) % D], n0, kof(kt + 1 + D), kend, tid);
+                __syncthreads();
+            }
+        }
+        // Drain the (unused) loads still in flight.
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+
+    const int z = blockIdx.z;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < p.M) p.store(m, n, z, acc[i][j][r]);
+            }
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int D, class P>
+hipError_t launch_igemm_pipe(const P& p, int splits, hipStream_t stream) {
+    using Cfg = TileCfg<BM, BN, BK, WM, WN>;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    dim3 grid(tiles_m * p.tiles_n, 1, splits);
+    auto kern = igemm_pipe_kernel<BM, BN, BK, WM, WN, D, P>;
+    if (Cfg::LDS_BYTES > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Cfg::LDS_BYTES);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), Cfg::LDS_BYTES, stream, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Warp-specialised variant for large tiles: CWM x CWN consumer waves run the
 // MFMAs of K slice t from LDS stage t&1 while NPW producer waves round slice
 // t+1 (loaded into their registers during slice t-1) to fp16 into stage

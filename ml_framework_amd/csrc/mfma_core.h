@@ -169,17 +169,22 @@ struct StageKC {
 };
 
 // MN-contiguous operand: element (row, k) at base[k * ld + row]. Each thread
-// owns an 8(k) x 4(row) block, loads it as 8 row-vectors and transposes it in
-// registers into 4 K-contiguous LDS rows. Consecutive threads take
-// consecutive row groups so a wave reads contiguous memory. VEC=4 needs the
-// row extent % 4 == 0, ld % 4 == 0 and a 16-byte aligned base.
+// owns a KK(k) x 4(row) block, loads it as KK row-vectors and transposes it in
+// registers into KK-half pieces of 4 K-contiguous LDS rows. KK is 8 (one
+// 16-byte chunk per row) when the tile has at least one such block per
+// thread; smaller tiles use KK = 4 or 2 so that every thread holds a block:
+// with KK = 8 the threads past the tile's blocks would idle while one wave
+// issued all of the tile's loads. Consecutive threads take consecutive row
+// groups so a wave reads contiguous memory. VEC=4 needs the row extent % 4 ==
+// 0, ld % 4 == 0 and a 16-byte aligned base.
 template <int ROWS, int BK, int NT, int VEC>
 struct StageMNC {
     static constexpr int CG = ROWS / 4;
-    static constexpr int KG = BK / 8;
+    static constexpr int KK = CG * BK / 8 >= NT ? 8 : (CG * BK / 4 >= NT ? 4 : 2);
+    static constexpr int KG = BK / KK;
     static constexpr int ITEMS = CG * KG;
     static constexpr int PASSES = (ITEMS + NT - 1) / NT;
-    float v[PASSES][8][4];
+    float v[PASSES][KK][4];
 
     __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld,
                                          int r0, int rmax, int k0, int kmax, int tid) {
@@ -188,10 +193,10 @@ struct StageMNC {
         for (int p = 0; p < PASSES; ++p) {
             const int item = p * NT + tid;
             const int dr = (item % CG) * 4;
-            const int dk = (item / CG) * 8;
+            const int dk = (item / CG) * KK;
             const bool live = ITEMS % NT == 0 || item < ITEMS;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < KK; ++j) {
                 const bool kin = live && k0 + dk + j < kmax;
                 const uint32_t off = (uint32_t)((dk + j) * ld + dr) * 4u;
                 if constexpr (VEC == 4) {
@@ -216,13 +221,23 @@ struct StageMNC {
             const int item = p * NT + tid;
             if (ITEMS % NT == 0 || item < ITEMS) {
                 const int row = (item % CG) * 4;
-                const int chunk = item / CG;
+                const int dk = (item / CG) * KK;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    float col[8];
+                    if constexpr (KK == 8) {
+                        float col[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) col[j] = v[p][j][q];
-                    lds_write8<BK>(tile, row + q, chunk, pack8(col));
+                        for (int j = 0; j < 8; ++j) col[j] = v[p][j][q];
+                        lds_write8<BK>(tile, row + q, dk / 8, pack8(col));
+                    } else {
+                        // KK halves at k = dk .. dk+KK-1 of row + q: a piece of
+                        // the row's 16-byte chunk dk / 8.
+                        typedef _Float16 halfk __attribute__((ext_vector_type(KK)));
+                        halfk h;
+#pragma unroll
+                        for (int j = 0; j < KK; ++j) h[j] = to_half(v[p][j][q]);
+                        *reinterpret_cast<halfk*>(tile + lds_off<BK>(row + q, dk / 8) + dk % 8) = h;
+                    }
                 }
             }
         }

@@ -27,6 +27,7 @@ constexpr int kNumCUs = 256;
 constexpr int kBK = 32;      // split-K slice granularity (slice ends are predicated, so it need
                              // not be a multiple of the tile BK; it is a multiple of 4 floats)
 constexpr int kMaxBK = 32;   // deepest K slice of any tile (tile span checks)
+constexpr int kPipeDepth = 2;  // K slices of loads in flight in igemm_pipe_kernel (4 measured no faster)
 
 inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
 inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
@@ -102,8 +103,24 @@ struct has_epi : std::false_type {};
 template <class P>
 struct has_epi<P, std::void_t<decltype(P::kEpi)>> : std::bool_constant<P::kEpi> {};
 
+// Problems whose stagers load without branches (a fixed load count per
+// slice) declare `static constexpr bool kPipe = true` and run the smaller
+// tiles on igemm_pipe_kernel (several K slices of loads in flight).
+template <class P, class = void>
+struct pipe_ok : std::false_type {};
+template <class P>
+struct pipe_ok<P, std::void_t<decltype(P::kPipe)>> : std::bool_constant<P::kPipe> {};
+
 template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
+    if constexpr (pipe_ok<P>::value) {
+        switch (t) {
+            case Tile::W: return launch_igemm_pipe<64, 256, 32, 1, 4, kPipeDepth>(p, splits, st);
+            case Tile::M: return launch_igemm_pipe<128, 128, 32, 2, 2, kPipeDepth>(p, splits, st);
+            case Tile::S: return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
+            default: break;
+        }
+    }
     if constexpr (BIG) {
         switch (t) {
             case Tile::L:
