@@ -160,9 +160,16 @@ def bench_conv(steps, warmup, stream):
     def bias_grad():
         capi.check(lib.seera_hip_conv_bias_grad_async(pdy.ptr, pdb.ptr, N, F, H * W, stream.ptr))
 
+    def bwd_bias():
+        # The layer's backward with its bias: db from the dW pass's reads of dY.
+        capi.check(lib.seera_hip_conv2d_bwd_bias_async(pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr,
+                                                       pdb.ptr, N, C, H, W, F, 3, 3, 1, 1, 1, 1,
+                                                       stream.ptr))
+
     res = {"ms_fwd": timed(fwd, steps, warmup, stream), "ms_bwd": timed(bwd, steps, warmup, stream),
            "ms_fwd_fused_bias_relu": timed(fwd_fused, steps, warmup, stream),
-           "ms_bias_grad": timed(bias_grad, steps, warmup, stream)}
+           "ms_bias_grad": timed(bias_grad, steps, warmup, stream),
+           "ms_bwd_with_bias_grad": timed(bwd_bias, steps, warmup, stream)}
     for v in (px, pw, pdy, py, pdx, pdw, pb, pm, pdb):
         v.close()
     return res
@@ -605,6 +612,7 @@ def main():
             "ms_fwd": round(cv["ms_fwd"], 4), "ms_bwd": round(cv["ms_bwd"], 4),
             "ms_fwd_fused_bias_relu": round(cv["ms_fwd_fused_bias_relu"], 4),
             "ms_bias_grad": round(cv["ms_bias_grad"], 4),
+            "ms_bwd_with_bias_grad": round(cv["ms_bwd_with_bias_grad"], 4),
             # Algorithmic HBM bytes: fwd reads X, writes Y (2 x 102.8 MB); bwd's
             # dX pass reads dY, writes dX and its dW pass reads X and dY (4 x).
             "fwd_hbm_frac": round(2 * 102.76e6 / (cv["ms_fwd"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),

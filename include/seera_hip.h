@@ -232,6 +232,27 @@ int seera_hip_conv2d_bwd_async(const float *W, const float *X, const float *dY,
                                int W_in, int N, int R, int S, int strideh,
                                int stridew, int padh, int padw, void *stream);
 
+/* No single counterpart in the reference: a Conv2D layer's backward with its
+ * bias. The reference runs cuda_conv2d_bwd (convolution.cu:393-453) and, for
+ * the bias, reduces dY to [1, N, 1, 1] with three cuten.sum calls
+ * (Seera_Engine.py:42-65; reductionKernels.cu:12-29). Here dX and dW are
+ * those of seera_hip_conv2d_bwd (same kernels, same bits) and db[n] = sum of
+ * dY over images and pixels is taken from the fp32 dY values as the
+ * weight-gradient pass loads them (stride-1 convolutions whose rows fit its
+ * tiles; other shapes take a separate fixed-order pass), so dY is not read a
+ * second time. db sums in a fixed order (deterministic; another order than
+ * the reference's). Argument order as seera_hip_conv2d_bwd, db after dW. */
+int seera_hip_conv2d_bwd_bias(const float *W, const float *X, const float *dY,
+                              float *dX, float *dW, float *db, int batch,
+                              int C, int H, int W_in, int N, int R, int S,
+                              int strideh, int stridew, int padh, int padw);
+int seera_hip_conv2d_bwd_bias_async(const float *W, const float *X,
+                                    const float *dY, float *dX, float *dW,
+                                    float *db, int batch, int C, int H,
+                                    int W_in, int N, int R, int S,
+                                    int strideh, int stridew, int padh,
+                                    int padw, void *stream);
+
 /* ---- ConvTranspose2D: engine_cuda/src/upsampling.cu ---- */
 
 /* cuda_conv2DTranpose_fwd [sic] (upsampling.cu:376-401; binding

@@ -64,6 +64,8 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_conv2d_fwd_async": (_conv14 + [_vp], _i),
     "seera_hip_conv2d_bwd": (_conv16, _i),
     "seera_hip_conv2d_bwd_async": (_conv16 + [_vp], _i),
+    "seera_hip_conv2d_bwd_bias": ([_vp] * 6 + [_i] * 11, _i),
+    "seera_hip_conv2d_bwd_bias_async": ([_vp] * 6 + [_i] * 11 + [_vp], _i),
     "seera_hip_conv2DTranpose_fwd": (_conv14, _i),
     "seera_hip_conv2DTranpose_fwd_async": (_conv14 + [_vp], _i),
     "seera_hip_conv2DTranspose_bwd": (_conv16, _i),

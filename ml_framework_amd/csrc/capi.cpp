@@ -176,7 +176,25 @@ int conv2d_bwd_impl(const float* Wt, const float* X, const float* dY, float* dX,
     const int Ho = conv_out(H, padh, R, strideh), Wo = conv_out(W_in, padw, S, stridew);
     SEERA_TRY(conv_dgrad(dY, Wt, dX, batch, N, Ho, Wo, C, H, W_in, R, S, strideh, stridew, padh,
                          padw, st));
-    return conv_wgrad(dY, X, dW, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw, st);
+    return conv_wgrad(dY, X, dW, nullptr, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw,
+                      st);
+}
+
+int conv2d_bwd_bias_impl(const float* Wt, const float* X, const float* dY, float* dX, float* dW,
+                         float* db, int batch, int C, int H, int W_in, int N, int R, int S,
+                         int strideh, int stridew, int padh, int padw, hipStream_t st) {
+    if (!db) return fail(SEERA_ERR_INVALID_ARGUMENT, "null device pointer (db)");
+    SEERA_TRY(check_conv_geometry(R, S, strideh, stridew, padh, padw));
+    if (batch < 0 || C < 1 || H < 1 || W_in < 1 || N < 1)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_bwd: bad tensor dims");
+    if (H + 2 * padh < R || W_in + 2 * padw < S)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_bwd: kernel larger than padded input");
+    SEERA_TRY(check_ptrs(true, Wt, dW, batch > 0 ? X : dW, batch > 0 ? dY : dW,
+                         batch > 0 ? dX : dW));
+    const int Ho = conv_out(H, padh, R, strideh), Wo = conv_out(W_in, padw, S, stridew);
+    SEERA_TRY(conv_dgrad(dY, Wt, dX, batch, N, Ho, Wo, C, H, W_in, R, S, strideh, stridew, padh,
+                         padw, st));
+    return conv_wgrad(dY, X, dW, db, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw, st);
 }
 
 int convT_dims(int Hin, int Win, int KH, int KW, int sh, int sw, int ph, int pw, int* Hout,
@@ -218,7 +236,7 @@ int convT_bwd_impl(const float* Wt, const float* X, const float* dY, float* dX, 
     SEERA_TRY(conv_fwd(dY, Wt, dX, batch, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, st));
     // dW[ci, co, kh, kw] = sum X[b, ci, hi, wi] dY[b, co, hi*sh-ph+kh, wi*sw-pw+kw]:
     // the conv weight gradient with X in the role of dY and dY in that of X.
-    return conv_wgrad(X, dY, dW, batch, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, st);
+    return conv_wgrad(X, dY, dW, nullptr, batch, Cout, Hout, Wout, Cin, KH, KW, sh, sw, ph, pw, st);
 }
 
 template <class F>
@@ -472,6 +490,24 @@ int seera_hip_conv2d_bwd(const float* W, const float* X, const float* dY, float*
     return guarded([&] {
         return sync_after(conv2d_bwd_impl(W, X, dY, dX, dW, batch, C, H, W_in, N, R, S, strideh,
                                           stridew, padh, padw, nullptr));
+    });
+}
+
+int seera_hip_conv2d_bwd_bias(const float* W, const float* X, const float* dY, float* dX,
+                              float* dW, float* db, int batch, int C, int H, int W_in, int N,
+                              int R, int S, int strideh, int stridew, int padh, int padw) {
+    return guarded([&] {
+        return sync_after(conv2d_bwd_bias_impl(W, X, dY, dX, dW, db, batch, C, H, W_in, N, R, S,
+                                               strideh, stridew, padh, padw, nullptr));
+    });
+}
+int seera_hip_conv2d_bwd_bias_async(const float* W, const float* X, const float* dY, float* dX,
+                                    float* dW, float* db, int batch, int C, int H, int W_in,
+                                    int N, int R, int S, int strideh, int stridew, int padh,
+                                    int padw, void* stream) {
+    return guarded([&] {
+        return queued(conv2d_bwd_bias_impl(W, X, dY, dX, dW, db, batch, C, H, W_in, N, R, S,
+                                           strideh, stridew, padh, padw, as_stream(stream)));
     });
 }
 

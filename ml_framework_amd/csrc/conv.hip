@@ -385,8 +385,8 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     return run_plan<true>(fill(PixelProblem<1, DgradGather>{}), pl, st);
 }
 
-int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
-               int R, int S, int sh, int sw, int ph, int pw, hipStream_t st) {
+int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H, int W,
+               int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st) {
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
     const int64_t npix = (int64_t)B * Ho * Wo, crs = (int64_t)C * R * S;
     if (npix > 0x7fffffff || crs > 0x7fffffff)
@@ -402,17 +402,23 @@ int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, i
     p.ldc = crs;
     p.split_stride = 0;
     if (npix == 0) {
-        // Empty contraction: dW = 0.
+        // Empty contraction: dW = 0 (and db = 0).
         SEERA_TRY(fill_f32(dW, 0.f, (size_t)F * crs, st));  // a kernel: safe under graph capture
+        if (db) SEERA_TRY(fill_f32(db, 0.f, (size_t)F, st));
         return SEERA_OK;
     }
-    bool used = false;
-    SEERA_TRY(band_conv_wgrad(Y, X, dW, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used));
-    if (used) return SEERA_OK;
-    // Gather path: any width, any kernel size.
-    // Gathers only: the 64x64 tile, split over pixels.
-    const Plan pl = plan_tiles(F, (int)crs, (int)npix, false, true);
-    return run_plan<false>(p, pl, st);
+    bool used = false, db_done = false;
+    SEERA_TRY(band_conv_wgrad(Y, X, dW, db, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used,
+                              &db_done));
+    if (!used) {
+        // Gather path: any width, any kernel size.
+        // Gathers only: the 64x64 tile, split over pixels.
+        const Plan pl = plan_tiles(F, (int)crs, (int)npix, false, true);
+        SEERA_TRY(run_plan<false>(p, pl, st));
+    }
+    // Paths that do not fuse the bias gradient: its own pass over dY.
+    if (db && !db_done) return conv_bias_grad(Y, db, B, F, Ho * Wo, st);
+    return SEERA_OK;
 }
 
 }  // namespace seera

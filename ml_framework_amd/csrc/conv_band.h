@@ -98,18 +98,23 @@ struct WgradArgs {
 // (conv_wgrad.hip): part[tile][split][64 f][CT*R*S], column (r*S + s)*CT + c.
 struct WgradPartials {
     float* part;
+    float* dbpart;  // [ftiles][nsplit][64] bias-gradient partials, or nullptr
     int CT, nctile, ntiles, nsplit;
 };
 
 // Row-streaming dW partials of a stride-1 convolution (R, S <= 3, rows
-// float4-aligned); *used reports whether it ran. The caller reduces them.
+// float4-aligned), and with with_db the bias-gradient partials of dY; *used
+// reports whether it ran. The caller reduces them.
 int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,
-                          int R, int S, int ph, int pw, hipStream_t st, WgradPartials* out,
-                          bool* used);
+                          int R, int S, int ph, int pw, bool with_db, hipStream_t st,
+                          WgradPartials* out, bool* used);
 
 // dW [F, C, R, S] = sum over (b, oh, ow) of dY[b, f, oh, ow] *
-// X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies.
-int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
-                    int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used);
+// X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies. With a
+// non-null db and the row-streaming path, also db[f] = sum of dY[b, f, ...]
+// from the same pass (*db_done reports it; otherwise the caller computes db).
+int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H,
+                    int W, int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st,
+                    bool* used, bool* db_done);
 
 }  // namespace seera

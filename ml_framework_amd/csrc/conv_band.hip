@@ -903,10 +903,37 @@ __global__ __launch_bounds__(kRedCols * kRedGroups) void wgrad_reduce(
 // groups with 16 loads in flight per thread were slower, 8.4-9.0 us). The
 // group sums are added in group order, as above.
 constexpr int kRed4Lanes = 64, kRed4Groups = 8, kRed4Unroll = 8;
+
+// The blocks past dW's (nb_dw of them) add the bias-gradient partials
+// dbpart[ftile][split][64]: db[f] = sum over splits in split order, as eight
+// groups of splits added in group order.
+__device__ void db_reduce_block(const float* __restrict__ dbpart, float* __restrict__ db, int F,
+                                int nsplit, int blk, floatx4 (*red)[kRed4Lanes]) {
+    const int lane = threadIdx.x % kRed4Lanes, grp = threadIdx.x / kRed4Lanes;
+    const int f = blk * 64 + lane;
+    const int per = (nsplit + kRed4Groups - 1) / kRed4Groups;
+    const int z0 = grp * per, z1 = min(nsplit, z0 + per);
+    float acc = 0.f;
+    if (f < F)
+        for (int z = z0; z < z1; ++z) acc += dbpart[((int64_t)blk * nsplit + z) * 64 + lane];
+    red[grp][lane][0] = acc;
+    __syncthreads();
+    if (grp != 0 || f >= F) return;
+    float sum = red[0][lane][0];
+#pragma unroll
+    for (int g = 1; g < kRed4Groups; ++g) sum += red[g][lane][0];
+    db[f] = sum;
+}
+
 __global__ __launch_bounds__(kRed4Lanes * kRed4Groups) void wgrad_reduce4(
     const float* __restrict__ part, float* __restrict__ dW, int F, int C, int R, int S, int CT,
-    int nctile, int ntiles, int nsplit) {
+    int nctile, int ntiles, int nsplit, const float* __restrict__ dbpart, float* __restrict__ db,
+    int nb_dw) {
     __shared__ floatx4 red[kRed4Groups][kRed4Lanes];
+    if ((int)blockIdx.x >= nb_dw) {
+        db_reduce_block(dbpart, db, F, nsplit, (int)blockIdx.x - nb_dw, red);
+        return;
+    }
     const int ntot = CT * R * S;
     const int lane = threadIdx.x % kRed4Lanes, grp = threadIdx.x / kRed4Lanes;
     const int64_t i = ((int64_t)blockIdx.x * kRed4Lanes + lane) * 4;  // first of 4 columns
@@ -947,16 +974,22 @@ __global__ __launch_bounds__(kRed4Lanes * kRed4Groups) void wgrad_reduce4(
     }
 }
 
-// Adds the partials of `ntiles` (tile, filter) rows of CT*R*S columns.
+// Adds the partials of `ntiles` (tile, filter) rows of CT*R*S columns, and
+// with dbpart the bias-gradient partials into db (CT*R*S % 4 == 0 only: the
+// stride-1 row-streaming path, whose tiles are 64 channels wide).
 hipError_t launch_wgrad_reduce(const float* part, float* dW, int F, int C, int R, int S, int CT,
-                               int nctile, int ntiles, int nsplit, hipStream_t st) {
+                               int nctile, int ntiles, int nsplit, hipStream_t st,
+                               const float* dbpart, float* db) {
     const int64_t total = (int64_t)ntiles * 64 * CT * R * S;
     if ((CT * R * S) % 4 == 0) {
         const int64_t cols = kRed4Lanes * 4;
-        hipLaunchKernelGGL(wgrad_reduce4, dim3((unsigned)((total + cols - 1) / cols)),
+        const int nb_dw = (int)((total + cols - 1) / cols);
+        const int nb_db = dbpart ? (F + 63) / 64 : 0;
+        hipLaunchKernelGGL(wgrad_reduce4, dim3((unsigned)(nb_dw + nb_db)),
                            dim3(kRed4Lanes * kRed4Groups), 0, st, part, dW, F, C, R, S, CT,
-                           nctile, ntiles, nsplit);
+                           nctile, ntiles, nsplit, dbpart, db, nb_dw);
     } else {
+        if (dbpart) return hipErrorInvalidValue;  // not produced on this path
         hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((total + kRedCols - 1) / kRedCols)),
                            dim3(kRedCols * kRedGroups), 0, st, part, dW, F, C, R, S, CT, nctile,
                            ntiles, nsplit);
@@ -1107,18 +1140,22 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
 }
 
 
-int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
-                    int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used) {
+int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H,
+                    int W, int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st,
+                    bool* used, bool* db_done) {
     *used = false;
+    *db_done = false;
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
     if (sh == 1 && sw == 1) {
         WgradPartials wp{};
         bool streamed = false;
-        SEERA_TRY(stream_wgrad_partials(Y, X, B, C, H, W, F, R, S, ph, pw, st, &wp, &streamed));
+        SEERA_TRY(stream_wgrad_partials(Y, X, B, C, H, W, F, R, S, ph, pw, db != nullptr, st, &wp,
+                                        &streamed));
         if (streamed) {
             SEERA_HIP_TRY(launch_wgrad_reduce(wp.part, dW, F, C, R, S, wp.CT, wp.nctile, wp.ntiles,
-                                              wp.nsplit, st));
+                                              wp.nsplit, st, wp.dbpart, db));
             *used = true;
+            *db_done = wp.dbpart != nullptr;
             return SEERA_OK;
         }
     }
@@ -1190,7 +1227,8 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int
     if (sw == 1) e = nch == 2 ? launch_wgrad_sw<1, 2>(a, ngw, st) : launch_wgrad_sw<1, 1>(a, ngw, st);
     else e = nch == 2 ? launch_wgrad_sw<2, 2>(a, ngw, st) : launch_wgrad_sw<2, 1>(a, ngw, st);
     if (e != hipSuccess) return fail_hip(e, "band wgrad launch");
-    SEERA_HIP_TRY(launch_wgrad_reduce(a.part, dW, F, C, R, S, a.CT, a.nctile, tiles, a.nsplit, st));
+    SEERA_HIP_TRY(launch_wgrad_reduce(a.part, dW, F, C, R, S, a.CT, a.nctile, tiles, a.nsplit, st,
+                                      nullptr, nullptr));
     *used = true;
     return SEERA_OK;
 }

@@ -15,7 +15,11 @@
 //     (v_alignbit), so the ring holds each X row once.
 // Each block writes its partial; wgrad_reduce (conv_band.hip) adds them in a
 // fixed order. HBM sees each dY element once and each X row once per strip
-// plus R-1 halo rows.
+// plus R-1 halo rows. With the bias gradient requested, the producers also
+// sum every dY element they load (fp32, before rounding) and each block
+// writes 64 per-filter partials that the same reduce adds up: db[f] = sum of
+// dY over images and pixels (the reference's three cuten.sum calls,
+// Seera_Engine.py:42-65) without a second pass over dY.
 #include "conv_band.h"
 #include "mfma_core.h"
 
@@ -41,6 +45,7 @@ struct WStreamArgs {
     const float* dy;     // [B, F, Ho, Wo]
     const float* x;      // [B, C, H, W]
     float* part;         // [tiles][nsplit][64][64*R*S]
+    float* dbpart;       // [ftiles][nsplit][64] bias-gradient partials (nullptr: none)
     int B, C, H, W, F, Ho, Wo, R, S, ph, pw;
     int L, nstrip, nsplit, nctile;
     int Wp;              // padded row length (pixels, multiple of 32)
@@ -216,6 +221,13 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                     for (int i = 0; i < 4; ++i)
                         dst[(int64_t)(32 * fh + 16 * fg + 4 * kc + i) * ntot + n] = acc[fg][r][s][i];
                 }
+        if (a.dbpart) {
+            // The producers' bias-gradient reduction reuses the rings once
+            // every consumer is done with them (both barriers are matched
+            // by the producers).
+            __syncthreads();
+            __syncthreads();
+        }
         return;
     }
 
@@ -266,6 +278,13 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     }
     floatx4 xv[kXI][3], dv[kDI][2];  // DD < 0: three aligned quads per X item
     float xw[kXI][8];                // DD >= 0: exactly the item's 8 floats
+    // Bias gradient: each dY item's fp32 values as they pass through the
+    // registers, one running sum per item (the item keeps its filter from
+    // step to step). Channel tiles other than the first see the same dY.
+    const bool db_on = a.dbpart != nullptr && ctile == 0;
+    float dsum[kDI];
+#pragma unroll
+    for (int k = 0; k < kDI; ++k) dsum[k] = 0.f;
 
     // Loads of X group rows [I0, I0 + NX) and dY output rows [O0, O0 + ND).
 #define SEERA_WG_LOAD(I0, NX, O0, ND)                                                      \
@@ -328,6 +347,9 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                     v8[q] = dv[k][0][q];                                                   \
                     v8[4 + q] = dv[k][1][q];                                               \
                 }                                                                          \
+                if (db_on) {                                                               \
+                    _Pragma("unroll") for (int q = 0; q < 8; ++q) dsum[k] += v8[q];        \
+                }                                                                          \
                 *reinterpret_cast<half8*>(dr + (o % (2 * kG)) * (kTile * a.rs) +           \
                                           dfl[k] * a.rs + dcol[k]) = pack8(v8);            \
             }                                                                              \
@@ -351,6 +373,21 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     }
 #undef SEERA_WG_LOAD
 #undef SEERA_WG_STORE
+    if (a.dbpart) {
+        __syncthreads();  // every consumer is past its last ring read
+        float* const red = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int k = 0; k < kDI; ++k) red[k * kProd + ptid] = dsum[k];
+        __syncthreads();
+        // Filter f's items are it = (row * 64 + f) * ndo + j (row < kG,
+        // j < ndo), stored at red[it]: summed in that order, from +0.
+        if (ctile == 0 && ptid < kTile) {
+            float sum = 0.f;
+            for (int row = 0; row < kG; ++row)
+                for (int j = 0; j < ndo; ++j) sum += red[(row * kTile + ptid) * ndo + j];
+            a.dbpart[((int64_t)ftile * a.nsplit + split) * kTile + ptid] = sum;
+        }
+    }
 }
 
 template <int RR>
@@ -385,8 +422,8 @@ int device_cus() {
 }  // namespace
 
 int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,
-                          int R, int S, int ph, int pw, hipStream_t st, WgradPartials* out,
-                          bool* used) {
+                          int R, int S, int ph, int pw, bool with_db, hipStream_t st,
+                          WgradPartials* out, bool* used) {
     *used = false;
     const int Ho = H + 2 * ph - R + 1, Wo = W + 2 * pw - S + 1;
     if (R < 1 || R > 3 || S < 1 || S > 3 || Ho <= 0 || Wo <= 0 || B <= 0) return SEERA_OK;
@@ -425,9 +462,15 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     }
     a.nstrip = (Ho + a.L - 1) / a.L;
     a.nsplit = B * a.nstrip;
+    // The kernel's producers reuse the rings for the bias-gradient reduction.
+    if (with_db && kProd * kDI * 4 > a.lds_bytes) return SEERA_OK;
+    const int nftile = (F + kTile - 1) / kTile;
+    const size_t part_n = (size_t)ntiles * a.nsplit * 64 * kTile * R * S;
+    const size_t db_n = with_db ? (size_t)nftile * a.nsplit * kTile : 0;
     void* ws = nullptr;
-    SEERA_TRY(workspace(sizeof(float) * (size_t)ntiles * a.nsplit * 64 * kTile * R * S, &ws, st));
+    SEERA_TRY(workspace(sizeof(float) * (part_n + db_n), &ws, st));
     a.part = static_cast<float*>(ws);
+    a.dbpart = with_db ? a.part + part_n : nullptr;
     hipError_t e;
     switch (R) {
         case 1: e = launch_rr<1>(a, ntiles, st); break;
@@ -436,6 +479,7 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     }
     if (e != hipSuccess) return fail_hip(e, "stream wgrad launch");
     out->part = a.part;
+    out->dbpart = a.dbpart;
     out->CT = kTile;
     out->nctile = a.nctile;
     out->ntiles = ntiles;

@@ -47,9 +47,11 @@ int conv_bias_grad(const float* dY, float* db, int B, int F, int HW, hipStream_t
 // out[B, C, H, W] = transposed conv of Y[B, F, Hi, Wi] with W[F, C, R, S].
 int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, int Hi, int Wi,
                int C, int H, int W, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
-// dW[F, C, R, S] = sum over (b, ho, wo) of Y[B, F, Ho, Wo] x im2col(X[B, C, H, W]).
-int conv_wgrad(const float* Y, const float* X, float* dW, int B, int C, int H, int W, int F,
-               int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
+// dW[F, C, R, S] = sum over (b, ho, wo) of Y[B, F, Ho, Wo] x im2col(X[B, C, H, W]);
+// with db non-null also db[F] = sum over (b, ho, wo) of Y (fused into the
+// stride-1 row-streaming pass, a separate fixed-order pass otherwise).
+int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H, int W,
+               int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
 
 // ---- tensor_ops.hip: the reference's element-wise, activation, softmax,
 // broadcast, unpooling and reduction functions ----

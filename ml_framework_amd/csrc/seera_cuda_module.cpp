@@ -166,6 +166,16 @@ PYBIND11_MODULE(seera_cuda, m) {
                   stride_h, stride_w, act));
           },
           "conv = act(conv2d(image, kernel) + bias[n]) (GPU ptrs, pad before stride)");
+    m.def("cuda_conv2d_bwd_bias",
+          [](uintptr_t W, uintptr_t X, uintptr_t dY, uintptr_t dX, uintptr_t dW, uintptr_t db,
+             int batch, int C, int H, int W_in, int N, int R, int S, int strideh, int stridew,
+             int padh, int padw) {
+              check(seera_hip_conv2d_bwd_bias(dev<const float>(W), dev<const float>(X),
+                                              dev<const float>(dY), dev<float>(dX),
+                                              dev<float>(dW), dev<float>(db), batch, C, H, W_in,
+                                              N, R, S, strideh, stridew, padh, padw));
+          },
+          "cuda_conv2d_bwd plus db = sum of dY per channel from the same pass (GPU ptrs)");
     m.def("cuda_conv_bias_grad",
           [](uintptr_t dY, uintptr_t db, int batchN, int N, int HW) {
               check(seera_hip_conv_bias_grad(dev<const float>(dY), dev<float>(db), batchN, N, HW));

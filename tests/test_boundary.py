@@ -203,6 +203,12 @@ def test_validation_fused_entry_points():
     st, msg = _status("seera_hip_conv2d_fwd_bias_act", 1, 1, None, 1, None, 1, 1, 2, 4, 1, 5, 3,
                       0, 1, 1, 1, 1)
     assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "larger" in msg, msg
+    st, msg = _status("seera_hip_conv2d_bwd_bias", 1, 1, 1, 1, 1, None, 2, 3, 8, 8, 4, 3, 3,
+                      1, 1, 1, 1)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "db" in msg, msg
+    st, msg = _status("seera_hip_conv2d_bwd_bias", 1, 1, 1, 1, 1, 1, 2, 3, 8, 8, 4, 3, 3,
+                      0, 1, 1, 1)
+    assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "stride" in msg, msg
     st, msg = _status("seera_hip_conv_bias_grad", 1, 1, -1, 4, 9)
     assert st == capi.SEERA_ERR_INVALID_ARGUMENT and "dims" in msg, msg
     st, msg = _status("seera_hip_matmul_bwd_relu", 1, 1, 1, None, 1, 1, 4, 4, 4, 1)

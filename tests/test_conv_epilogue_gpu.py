@@ -133,3 +133,70 @@ def test_fused_conv_against_oracle(case, act):
     if act == capi.SEERA_ACT_RELU:
         clear = np.abs(pre) > 1e-4 * np.sqrt(C * K * K)
         assert np.array_equal(mask[clear], (pre[clear] > 0).astype(np.float32))
+
+
+# (name, N, C, H, W, F, K, stride, pad): the first three take the fused
+# (row-streaming) dW + db pass, the others fall back to a separate db pass.
+BWD_BIAS = [
+    ("stream3x3_cfg4_b4", 4, 64, 56, 56, 64, 3, 1, 1),
+    ("stream3x3_2tiles", 3, 128, 20, 20, 96, 3, 1, 1),    # two filter and channel tiles
+    ("stream1x1", 5, 16, 12, 12, 8, 1, 1, 0),
+    ("band_s2", 4, 32, 32, 32, 64, 3, 2, 1),
+    ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),
+]
+
+
+@pytest.mark.parametrize("case", BWD_BIAS, ids=[c[0] for c in BWD_BIAS])
+def test_conv2d_bwd_bias(case):
+    """seera_hip_conv2d_bwd_bias: dX and dW bit-identical to
+    seera_hip_conv2d_bwd; db against an fp64 sum of dY over images and pixels
+    (the reference's three cuten.sum calls, Seera_Engine.py:42-65), and the
+    same bits on a second call (fixed summation order)."""
+    _, N, C, H, W, F, K, s, p = case
+    r = np.random.default_rng(N * 11 + C + F + K)
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (r.standard_normal((F, C, K, K)) * 0.2).astype(np.float32)
+    OH, OW = out_hw(H, W, K, K, s, p)
+    dy = r.standard_normal((N, F, OH, OW)).astype(np.float32)
+    args = (N, C, H, W, F, K, K, s, s, p, p)
+    with DeviceBuffer.from_array(w) as pw, DeviceBuffer.from_array(x) as px, \
+            DeviceBuffer.from_array(dy) as pdy, DeviceBuffer(x.nbytes) as pdx, \
+            DeviceBuffer(w.nbytes) as pdw, DeviceBuffer(x.nbytes) as pdx2, \
+            DeviceBuffer(w.nbytes) as pdw2, DeviceBuffer(F * 4) as pdb, DeviceBuffer(F * 4) as pdb2:
+        capi.call("seera_hip_conv2d_bwd", pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr, *args)
+        pdb.fill(0x7F)
+        capi.call("seera_hip_conv2d_bwd_bias", pw.ptr, px.ptr, pdy.ptr, pdx2.ptr, pdw2.ptr, pdb.ptr,
+                  *args)
+        capi.call("seera_hip_conv2d_bwd_bias", pw.ptr, px.ptr, pdy.ptr, pdx2.ptr, pdw2.ptr,
+                  pdb2.ptr, *args)
+        assert np.array_equal(pdx2.to_array(x.shape), pdx.to_array(x.shape))
+        assert np.array_equal(pdw2.to_array(w.shape), pdw.to_array(w.shape))
+        db, db2 = pdb.to_array((F,)), pdb2.to_array((F,))
+    assert np.array_equal(db, db2)
+    ref = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    bound = 1e-6 * np.abs(dy).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-6
+    assert np.all(np.abs(db - ref) <= bound), float(np.max(np.abs(db - ref) / bound))
+
+
+def test_conv2d_bwd_bias_config4():
+    """Config 4 at full size (N=128, 64->64, 56x56, 3x3 s1 p1): db from the
+    fused pass against an fp64 sum; dX and dW against the plain backward."""
+    r = np.random.default_rng(0)
+    N, C, H, W, F = 128, 64, 56, 56, 64
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = r.uniform(-np.sqrt(6 / 576), np.sqrt(6 / 576), (F, C, 3, 3)).astype(np.float32)
+    dy = r.standard_normal((N, F, H, W)).astype(np.float32)
+    args = (N, C, H, W, F, 3, 3, 1, 1, 1, 1)
+    with DeviceBuffer.from_array(w) as pw, DeviceBuffer.from_array(x) as px, \
+            DeviceBuffer.from_array(dy) as pdy, DeviceBuffer(x.nbytes) as pdx, \
+            DeviceBuffer(w.nbytes) as pdw, DeviceBuffer(x.nbytes) as pdx2, \
+            DeviceBuffer(w.nbytes) as pdw2, DeviceBuffer(F * 4) as pdb:
+        capi.call("seera_hip_conv2d_bwd", pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr, *args)
+        capi.call("seera_hip_conv2d_bwd_bias", pw.ptr, px.ptr, pdy.ptr, pdx2.ptr, pdw2.ptr, pdb.ptr,
+                  *args)
+        assert np.array_equal(pdx2.to_array(x.shape), pdx.to_array(x.shape))
+        assert np.array_equal(pdw2.to_array(w.shape), pdw.to_array(w.shape))
+        db = pdb.to_array((F,))
+    ref = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    bound = 1e-6 * np.abs(dy).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-6
+    assert np.all(np.abs(db - ref) <= bound), float(np.max(np.abs(db - ref) / bound))
