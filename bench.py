@@ -506,6 +506,16 @@ def traffic_from_profiles():
     return None
 
 
+# Single workloads for the per-kernel rocprofv3 passes (bench.py --workload NAME).
+WORKLOADS = {
+    "gemm1024": lambda steps, warmup, st: bench_gemm(1024, steps, warmup, st, True),
+    "gemm2048": lambda steps, warmup, st: bench_gemm(2048, steps, warmup, st, True),
+    "gemm4096": lambda steps, warmup, st: bench_gemm(4096, steps, warmup, st, False),
+    "mlp_cfg3": bench_mlp,
+    "conv2d_cfg4": bench_conv,
+    "convT_cfg5": bench_convT,
+}
+
 # Algorithmic HBM bytes of one forward + backward, counted at the API: each
 # call reads its inputs once and writes its outputs once (fp32), nothing else.
 #   Conv2D config 4: fwd X, W -> Y; bwd W, X, dY -> dX, dW.
@@ -546,6 +556,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run device copies of BYTES (counter calibration), then exit")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default=None,
+                    help="only run this workload (--steps timed calls) and print its timings: "
+                         "the command the per-kernel rocprofv3 passes profile")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU "
@@ -557,6 +570,12 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.workload:
+        stream = Stream()
+        res = WORKLOADS[args.workload](args.steps, args.warmup, stream)
+        print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup,
+                          **{k: v for k, v in res.items() if isinstance(v, (int, float, str))}}))
         return
 
     stream = Stream()
