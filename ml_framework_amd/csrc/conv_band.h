@@ -68,6 +68,16 @@ int band_conv_dgrad(const float* Y, const float* W, float* out, int B, int Fc, i
                     int Cc, int H, int W_out, int R, int S, int sh, int sw, int ph, int pw,
                     hipStream_t st, bool* used);
 
+// Stride-2 transposed convolution of band_conv_dgrad's form with all four
+// stride phases per block (conv_phase2.hip): in [B, C, H, W], W [C, F, R, S]
+// read at taps (r0h[a] + 2*(T[a]-1-t), r0w[c] + 2*(U[c]-1-u)), out [B, F,
+// Hout, Wout]; runs when C % 32 == 0, C <= 128, T, U in {1, 2}, Hout even and
+// Wout % 8 == 0; *used reports whether it ran.
+int phase2_conv(const float* in, const float* W, float* out, int B, int C, int H, int W_in, int F,
+                int Hout, int Wout, int R, int S, const int T[2], const int iph[2],
+                const int r0h[2], const int U[2], const int ipw[2], const int r0w[2],
+                hipStream_t st, bool* used);
+
 // Row-streaming variant (conv_stream.hip) of the launch `band` describes
 // (weights already prepared in band.wk): runs when every phase reads its input
 // with stride 1 and the weights plus an input-row ring fit in LDS; *used

@@ -1111,6 +1111,20 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
             woff += (int64_t)a.nftiles * a.nchunks * xh.T * xw.T * 2048;
         }
     a.nphase = zi;
+    if (sh == 2 && sw == 2) {
+        // All four stride phases in one block (conv_phase2.hip) when it applies.
+        const int T2[2] = {ax[0][0].T, ax[2][0].T}, iph2[2] = {a.ph[0].iph, a.ph[2].iph};
+        const int r0h2[2] = {ax[0][0].r0, ax[2][0].r0};
+        const int U2[2] = {ax[0][1].T, ax[1][1].T}, ipw2[2] = {a.ph[0].ipw, a.ph[1].ipw};
+        const int r0w2[2] = {ax[0][1].r0, ax[1][1].r0};
+        bool done = false;
+        SEERA_TRY(phase2_conv(Yin, Wconv, out, B, Fc, Hi, Wi, Cc, H, W, R, S, T2, iph2, r0h2, U2,
+                              ipw2, r0w2, st, &done));
+        if (done) {
+            *used = true;
+            return SEERA_OK;
+        }
+    }
     if (!plan_tile(a)) return SEERA_OK;
     if (woff > 0x7fffffff) return SEERA_OK;  // prep kernel indexes in 32 bits
     void* ws = nullptr;

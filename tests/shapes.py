@@ -71,6 +71,16 @@ CONV2D_EDGE = [
     ("e08", 1, 65, 9, 9, 129, 3, 3, 2, 1),
 ]
 
+# Stride-2 shapes for the kernel that runs all four stride phases per block
+# (not from the reference's tests): the dX pass of a stride-2 convolution with
+# 3x3, 4x4 and 2x2 kernels, 1-3 channel chunks of dY, two column tiles of the
+# dX output, partial filter tiles.
+CONV2D_PHASE2 = [
+    ("q01", 2, 24, 16, 48, 96, 3, 3, 2, 1),    # T, U in {1, 2}, 3 chunks
+    ("q02", 2, 40, 20, 80, 32, 4, 4, 2, 1),    # 40 phase columns: two column tiles
+    ("q03", 3, 16, 12, 16, 64, 2, 2, 2, 0),    # one tap per phase
+]
+
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
 CONVT = [
     ("t01", 2, 4, 4, 4, 8, 3, 3, 1, 0),
@@ -94,6 +104,16 @@ CONVT = [
     ("t19", 2, 4, 4, 4, 8, 3, 3, 2, 1),
     # Testing/test_3.py:100-136 -- large convT, 4x4 s2 p1
     ("big_t", 8, 64, 32, 32, 32, 4, 4, 2, 1),
+]
+
+# Transposed shapes for the four-phase kernel (not from the reference's
+# tests): one and three input-channel chunks, 36 phase columns (two column
+# tiles), 40 output channels (a partial 32-filter tile), a 2x2 kernel.
+CONVT_PHASE2 = [
+    ("u01", 2, 32, 6, 20, 40, 4, 4, 2, 1),
+    ("u02", 2, 96, 10, 36, 24, 4, 4, 2, 1),
+    ("u03", 3, 64, 8, 8, 16, 2, 2, 2, 0),
+    ("u04", 1, 128, 28, 28, 64, 4, 4, 2, 1),   # one image of config 5
 ]
 
 # (M, K, N, Nbatch): Testing/test_2.py:372-375, Testing/test_14.py:148-183,

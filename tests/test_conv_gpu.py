@@ -12,7 +12,7 @@ from ml_framework_amd import capi
 from oracle import fp16r
 from tests.helpers import (assert_parity, hip_conv_bwd, hip_conv_fwd, hip_convT_bwd,
                            hip_convT_fwd, rel_fro)
-from tests.shapes import CONV2D, CONV2D_EDGE, CONV2D_STREAM, CONVT
+from tests.shapes import CONV2D, CONV2D_EDGE, CONV2D_PHASE2, CONV2D_STREAM, CONVT, CONVT_PHASE2
 
 pytestmark = pytest.mark.gpu
 S = oracle.seera_cpp
@@ -29,7 +29,8 @@ def _kaiming(r, shape, fan_in):
     return r.uniform(-lim, lim, shape).astype(np.float32)
 
 
-ALL_CONV2D = CONV2D + CONV2D_STREAM + CONV2D_EDGE
+ALL_CONV2D = CONV2D + CONV2D_STREAM + CONV2D_EDGE + CONV2D_PHASE2
+ALL_CONVT = CONVT + CONVT_PHASE2
 
 
 @pytest.mark.parametrize("case", ALL_CONV2D, ids=[c[0] for c in ALL_CONV2D])
@@ -50,7 +51,7 @@ def test_conv2d_parity(case):
     assert rel_fro(dx, rdx) <= STRICT and rel_fro(dw, rdw) <= STRICT
 
 
-@pytest.mark.parametrize("case", CONVT, ids=[c[0] for c in CONVT])
+@pytest.mark.parametrize("case", ALL_CONVT, ids=[c[0] for c in ALL_CONVT])
 def test_convT_parity(case):
     name, N, Cin, H, W, Cout, KH, KW, s, p = case
     r = np.random.default_rng(zlib.crc32(name.encode()))
