@@ -78,6 +78,12 @@ int phase2_conv(const float* in, const float* W, float* out, int B, int C, int H
                 const int r0h[2], const int U[2], const int ipw[2], const int r0w[2],
                 hipStream_t st, bool* used);
 
+// 4x4 convolution at stride 2, padding 1 (conv_stride2.hip): out [B, F, Ho,
+// Wo] of in [B, C, H, W] and W [F, C, 4, 4]; runs when C is 32 or 64, W % 4
+// == 0 and Wo % 4 == 0; *used reports whether it ran.
+int stride2_conv(const float* in, const float* W, float* out, int B, int C, int H, int W_in, int F,
+                 hipStream_t st, bool* used);
+
 // Row-streaming variant (conv_stream.hip) of the launch `band` describes
 // (weights already prepared in band.wk): runs when every phase reads its input
 // with stride 1 and the weights plus an input-row ring fit in LDS; *used

@@ -1042,6 +1042,15 @@ int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H
                   const ConvEpi& epi) {
     *used = false;
     if (W % 4 != 0 || !aligned16(X)) return SEERA_OK;
+    if (R == 4 && S == 4 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && !epi.bias && !epi.act) {
+        // Row streaming with column-parity planes (conv_stride2.hip) when it applies.
+        bool done = false;
+        SEERA_TRY(stride2_conv(X, Wt, Y, B, C, H, W, F, st, &done));
+        if (done) {
+            *used = true;
+            return SEERA_OK;
+        }
+    }
     BandConvArgs a{};
     a.in = X;
     a.out = Y;

@@ -71,14 +71,18 @@ CONV2D_EDGE = [
     ("e08", 1, 65, 9, 9, 129, 3, 3, 2, 1),
 ]
 
-# Stride-2 shapes for the kernel that runs all four stride phases per block
-# (not from the reference's tests): the dX pass of a stride-2 convolution with
-# 3x3, 4x4 and 2x2 kernels, 1-3 channel chunks of dY, two column tiles of the
-# dX output, partial filter tiles.
+# Stride-2 shapes for the four-phase and column-parity kernels (not from the
+# reference's tests): the dX pass of a stride-2 convolution with 3x3, 4x4 and
+# 2x2 kernels, 1-3 channel chunks of dY, two column tiles, partial filter
+# tiles, an odd input height.
 CONV2D_PHASE2 = [
     ("q01", 2, 24, 16, 48, 96, 3, 3, 2, 1),    # T, U in {1, 2}, 3 chunks
     ("q02", 2, 40, 20, 80, 32, 4, 4, 2, 1),    # 40 phase columns: two column tiles
     ("q03", 3, 16, 12, 16, 64, 2, 2, 2, 0),    # one tap per phase
+    # forward 4x4 s2 p1 by column-parity row streaming (32/64 input channels)
+    ("q04", 2, 64, 32, 64, 48, 4, 4, 2, 1),    # partial 64-filter tile
+    ("q05", 2, 32, 24, 88, 64, 4, 4, 2, 1),    # 44 output columns: two column tiles
+    ("q06", 1, 64, 17, 16, 32, 4, 4, 2, 1),    # odd input height
 ]
 
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
@@ -114,6 +118,7 @@ CONVT_PHASE2 = [
     ("u02", 2, 96, 10, 36, 24, 4, 4, 2, 1),
     ("u03", 3, 64, 8, 8, 16, 2, 2, 2, 0),
     ("u04", 1, 128, 28, 28, 64, 4, 4, 2, 1),   # one image of config 5
+    ("u05", 2, 96, 14, 20, 32, 4, 4, 2, 1),    # dX by column-parity streaming, one chunk
 ]
 
 # (M, K, N, Nbatch): Testing/test_2.py:372-375, Testing/test_14.py:148-183,
