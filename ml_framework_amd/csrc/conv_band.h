@@ -125,6 +125,12 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
                           int R, int S, int ph, int pw, bool with_db, hipStream_t st,
                           WgradPartials* out, bool* used);
 
+// Row-streaming dW partials of a 4x4 stride-2 padding-1 convolution
+// (conv_wgrad_s2.hip): Y [B, F, Ho, Wo], X [B, C, H, W]; runs when W and Wo
+// are multiples of 4; *used reports whether it ran. The caller reduces them.
+int wgrad_s2_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,
+                      hipStream_t st, WgradPartials* out, bool* used);
+
 // dW [F, C, R, S] = sum over (b, oh, ow) of dY[b, f, oh, ow] *
 // X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies. With a
 // non-null db and the row-streaming path, also db[f] = sum of dY[b, f, ...]

@@ -1182,6 +1182,17 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B,
             return SEERA_OK;
         }
     }
+    if (R == 4 && S == 4 && sh == 2 && sw == 2 && ph == 1 && pw == 1) {
+        WgradPartials wp{};
+        bool streamed = false;
+        SEERA_TRY(wgrad_s2_partials(Y, X, B, C, H, W, F, st, &wp, &streamed));
+        if (streamed) {
+            SEERA_HIP_TRY(launch_wgrad_reduce(wp.part, dW, F, C, R, S, wp.CT, wp.nctile, wp.ntiles,
+                                              wp.nsplit, st, nullptr, nullptr));
+            *used = true;
+            return SEERA_OK;
+        }
+    }
     if (Wo % 4 != 0 || W % 4 != 0 || sw > 2 || S > 7 || R * S > 18 || !aligned16(Y) ||
         !aligned16(X) || B == 0)
         return SEERA_OK;
