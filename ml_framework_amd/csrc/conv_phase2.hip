@@ -24,6 +24,8 @@
 // once per tap row and serves both column phases where their offsets meet.
 // HBM sees each input element once per 32-filter tile (plus halo rows) and
 // each output element once.
+#include <limits.h>
+
 #include "conv_band.h"
 #include "mfma_core.h"
 
@@ -393,9 +395,9 @@ int phase2_conv(const float* in, const float* Wt, float* out, int B, int C, int 
     a.in = in; a.out = out;
     a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Hout = Hout; a.Wout = Wout;
     a.nchunks = C / 32;
-    int emax = -1 << 30, dmax = -1 << 30;
-    a.emin = 1 << 30;
-    a.dmin = 1 << 30;
+    int emax = INT_MIN, dmax = INT_MIN;
+    a.emin = INT_MAX;
+    a.dmin = INT_MAX;
     for (int z = 0; z < 2; ++z) {
         a.T[z] = T[z]; a.iph[z] = iph[z]; a.U[z] = U[z]; a.ipw[z] = ipw[z];
         a.emin = std::min(a.emin, -iph[z]);
