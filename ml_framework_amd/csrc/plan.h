@@ -13,7 +13,8 @@ namespace seera {
 //   L   256x256x32, warp-specialised: 4x2 consumer waves of 64x128 run the
 //       MFMAs while 4 producer waves load and round the next K slice
 //   W   64x256x32,  1x4 waves of 64x64  few rows (conv output channels)
-//   M   128x128x32, 2x2 waves of 64x64
+//   M   128x128x32, 2x2 waves of 64x64 (warp-specialised, 2 producer waves,
+//       when the operands take streaming stagers)
 //   S   64x64x32,   2x2 waves of 32x32  small / odd shapes, scalar loads
 enum class Tile { L, W, M, S };
 
@@ -115,6 +116,14 @@ struct pipe_ok<P, std::void_t<decltype(P::kPipe)>> : std::bool_constant<P::kPipe
 
 template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
+    if constexpr (ws_stream<P>::value) {
+        // The 128x128 tile with warp-specialised producers (two waves per
+        // block, two K slices in flight): 2048^3 in 33 us against 44 us on
+        // the pipelined kernel below. The 64x64 and 64x256 tiles gain nothing
+        // or spill with a single producer wave, and keep the pipelined kernel.
+        if (t == Tile::M && p.K % 32 == 0)
+            return launch_igemm_ws2<128, 128, 32, 2, 2, 2>(p, splits, st);
+    }
     if constexpr (pipe_ok<P>::value) {
         switch (t) {
             case Tile::W: return launch_igemm_pipe<64, 256, 32, 1, 4, kPipeDepth>(p, splits, st);
