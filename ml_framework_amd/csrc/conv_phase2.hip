@@ -40,7 +40,11 @@ __device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c)
 }
 
 // Ring plane layout (as conv_stream.hip): pixel p holds 32 channels as four
-// 16-byte chunks, the chunk order rotated by (p >> 1) & 3.
+// 16-byte chunks, the chunk order rotated by (p >> 1) & 3. Producers write an
+// item's four pixels in pairs swapped on odd column quads: the 8 lanes of a
+// ds_write_b128 group (4 channel groups of two adjacent quads) then hit 8
+// distinct 16-byte slots of a 128-byte window (in quad order the two quads'
+// pixels sit 256 bytes apart, on the same 4 slots).
 __device__ __forceinline__ int ring_off(int p, int chunk) {
     return p * 32 + ((chunk ^ ((p >> 1) & 3)) << 3);
 }
@@ -188,12 +192,13 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
             const int i = r / NCH;
             if (it < nitems && i < need) {
                 half_t* dst = ring + (i % a.NR) * NCH * plane + ch * plane;
+                const int sw = q4 & 1;  // odd quads write their pixel pairs swapped
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int jj = 0; jj < 4; ++jj) {
                     float col[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) col[j] = xv[k][j][q];
-                    *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + q, cg)) = pack8(col);
+                    for (int j = 0; j < 8; ++j) col[j] = sw ? xv[k][j][jj ^ 1] : xv[k][j][jj];
+                    *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + (jj ^ sw), cg)) = pack8(col);
                 }
             }
         }
@@ -329,11 +334,13 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
             const int i = g0 + (G) * kRows + prow[k];                                        \
             if (prow[k] < kRows && i < need) {                                               \
                 half_t* dst = ring + (i % a.NR) * NCH * plane + pdst[k];                     \
-                _Pragma("unroll") for (int q = 0; q < 4; ++q) {                              \
+                const int sw = pq4[k] & 1;                                                   \
+                _Pragma("unroll") for (int jj = 0; jj < 4; ++jj) {                           \
                     float col[8];                                                            \
-                    _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = V[k][j][q];       \
+                    _Pragma("unroll") for (int j = 0; j < 8; ++j)                            \
+                        col[j] = sw ? V[k][j][jj ^ 1] : V[k][j][jj];                         \
                     /* = ring_off(4*q4 + q, cg) relative to pixel 4*q4 */                    \
-                    const int p = 4 * pq4[k] + q;                                            \
+                    const int q = jj ^ sw, p = 4 * pq4[k] + q;                               \
                     *reinterpret_cast<half8*>(dst + q * 32 + ((pcg[k] ^ ((p >> 1) & 3)) << 3)) = \
                         pack8(col);                                                          \
                 }                                                                            \

@@ -40,12 +40,15 @@ __device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c)
 }
 
 // Ring plane layout: pixel p holds 32 channels as four 16-byte chunks, the
-// chunk order rotated by (p >> 1) & 3. A ds_read_b128 is served per 32-lane
-// half-wave at 2 lanes per 16-byte slot of a 256-byte bank window per cycle,
-// and a ds_write_b128 per 8-lane group at 2 lanes per slot of a 128-byte
-// window (measured on gfx950); the B reads (16 consecutive pixels at each of
-// 2 chunks per half-wave, any start) and the item writes (4 channel groups x
-// 2 pixel quads per 8 lanes) both stay within that.
+// chunk order rotated by (p >> 1) & 3. Measured on gfx950: a ds_read_b128 is
+// served per 32-lane half-wave at 2 lanes per 16-byte slot of a 256-byte bank
+// window per cycle, which the B reads (16 consecutive pixels at each of 2
+// chunks per half-wave, any start) meet; a ds_write_b128 is conflict-free only
+// when the 8 lanes of each group hit 8 distinct 16-byte slots of a 128-byte
+// window. The item writes (4 channel groups of two adjacent column quads per
+// 8 lanes) meet that because odd quads write their four pixels with the pairs
+// swapped: in quad order the two quads' pixels sit 256 bytes apart, on the
+// same 4 slots.
 __device__ __forceinline__ int ring_off(int p, int chunk) {
     return p * 32 + ((chunk ^ ((p >> 1) & 3)) << 3);
 }
@@ -171,12 +174,14 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
             const int i = r / a.nchunks - sh;
             if (it < nitems && (unsigned)i < (unsigned)need) {
                 half_t* dst = ring + (i % a.NR) * a.nchunks * plane + ch * plane + q4 * 128;
+                const int sw = q4 & 1;  // odd quads write their pixel pairs swapped
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int jj = 0; jj < 4; ++jj) {
                     float col[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) col[j] = xv[k][j][q];
-                    *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + q, cg) - 4 * q4 * 32) = pack8(col);
+                    for (int j = 0; j < 8; ++j) col[j] = sw ? xv[k][j][jj ^ 1] : xv[k][j][jj];
+                    *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + (jj ^ sw), cg) - 4 * q4 * 32) =
+                        pack8(col);
                 }
             }
         }
@@ -459,10 +464,13 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
             const int i = (I0) + prow[k];                                                   \
             if (prow[k] < (NROWS) && (unsigned)i < (unsigned)need) {                        \
                 half_t* dst = ring + (i % a.NR) * a.nchunks * plane + pdst[k];              \
-                _Pragma("unroll") for (int q = 0; q < 4; ++q) {                             \
+                const int sw = prq[k] >> 1; /* odd quads: pixel pairs swapped */            \
+                _Pragma("unroll") for (int jj = 0; jj < 4; ++jj) {                          \
                     float col[8];                                                           \
-                    _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = V[k][j][q];      \
+                    _Pragma("unroll") for (int j = 0; j < 8; ++j)                           \
+                        col[j] = sw ? V[k][j][jj ^ 1] : V[k][j][jj];                        \
                     /* = ring_off(4*q4 + q, cg) relative to pixel 4*q4 */                   \
+                    const int q = jj ^ sw;                                                  \
                     *reinterpret_cast<half8*>(dst + q * 32 +                                \
                                               ((pcg[k] ^ ((prq[k] + (q >> 1)) & 3)) << 3)) = \
                         pack8(col);                                                         \

@@ -38,7 +38,10 @@ __device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c)
 }
 
 // Ring plane layout (as conv_stream.hip): pixel p holds 32 channels as four
-// 16-byte chunks, the chunk order rotated by (p >> 1) & 3.
+// 16-byte chunks, the chunk order rotated by (p >> 1) & 3. On odd column
+// quads the producers write the two pixels of a plane in swapped order, so the
+// 8 lanes of a ds_write_b128 group (4 channel groups of two adjacent quads)
+// hit 8 distinct 16-byte slots of a 128-byte window.
 __device__ __forceinline__ int ring_off(int p, int chunk) {
     return p * 32 + ((chunk ^ ((p >> 1) & 3)) << 3);
 }
@@ -208,10 +211,12 @@ __global__ __launch_bounds__(kNT) void stride2_conv_kernel(const Stride2Args a) 
 #define SEERA_S2_ITEM_WRITE(V, I, CH, CG, Q4)                                                \
     {                                                                                        \
         half_t* dst = ring + ((I) % kNR) * rowh + (CH) * plane;                              \
-        _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                      \
+        const int sw = ((Q4) & 1) << 1;  /* odd quads: the two pixels of a plane swapped */  \
+        _Pragma("unroll") for (int jj = 0; jj < 4; ++jj) {                                   \
             float col[8];                                                                    \
-            _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = V[j][q];                  \
+            _Pragma("unroll") for (int j = 0; j < 8; ++j) col[j] = sw ? V[j][jj ^ 2] : V[j][jj]; \
             /* column c0 + 4*q4 + q: parity q & 1, pixel 2*q4 + q/2 */                       \
+            const int q = jj ^ sw;                                                           \
             *reinterpret_cast<half8*>(dst + (q & 1) * NCH * plane +                          \
                                       ring_off(2 * (Q4) + (q >> 1), (CG))) = pack8(col);     \
         }                                                                                    \

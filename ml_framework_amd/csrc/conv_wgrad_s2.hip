@@ -36,8 +36,20 @@ constexpr int kCons = 4 * 64;
 constexpr int kProd = 256;
 constexpr int kNT = kCons + kProd;
 constexpr int kWC = 32;           // output columns per item (one K-slice)
-constexpr int kPx = 40;           // halves per LDS pixel row (80 bytes: 16 + a multiple of 64)
+// Halves per LDS pixel row: 96 bytes. A fragment read (16 rows x 4 chunks of
+// 16 bytes) is served per half-wave in two passes of 16 lanes, 8 rows x 2
+// chunks each; rows 96 bytes apart put those 16 lanes on 16 distinct 16-byte
+// slots of a 256-byte window (an 80-byte stride puts two lanes on a slot).
+constexpr int kPx = 48;
 constexpr int kNR = 2 * kIn + 2;  // ring rows of X
+
+// Row (filter or channel) of an LDS item from its index: bits 0 and 1 swapped,
+// so that the 8 lanes of a ds_write_b128 group (4 octets of rows r and r + 2,
+// 192 bytes apart) hit 8 distinct 16-byte slots of a 128-byte window (rows r
+// and r + 1, 96 bytes apart, put two lanes on each of two slots).
+__device__ __forceinline__ int item_row(int i) {
+    return (i & ~3) | ((i >> 1) & 1) | ((i & 1) << 1);
+}
 
 struct WgradS2Args {
     const float* y;      // [B, F, Ho, Wo]
@@ -127,7 +139,8 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
 
     // ---------------- producers ----------------
     // Y items: (row o, filter f, octet k): 8 pixels, 2 float4 loads; 512 per
-    // step, 2 per thread. X items: (input row, channel, octet k): the 24
+    // step, 2 per thread (filters in item_row order). X items: (input row,
+    // channel, octet k): the 24
     // columns 2*(ow0 + 8k) - 4 .. +23 (6 float4 loads), written as the four
     // frames' octets; 16*CT per step, CG per thread.
     const int ptid = tid - kCons;
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int it = ptid + k * kProd;  // (o, f, octet): octet fastest
-                const int oct = it & 3, f = (it >> 2) & 63, o = it >> 8;
+                const int oct = it & 3, f = item_row(it >> 2) & 63, o = it >> 8;
                 const int oh = oh0 + G * kRows + o, ow = ow0 + 8 * oct;
                 const bool ok = G * kRows + o < Lb && f < f_lim;
                 const uint32_t off = (uint32_t)(((f * a.Ho + oh) * a.Wo + ow) * 4);
@@ -166,7 +179,7 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int it = ptid + k * kProd;
-                const int oct = it & 3, f = (it >> 2) & 63, o = it >> 8;
+                const int oct = it & 3, f = item_row(it >> 2) & 63, o = it >> 8;
                 float v8[8];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -182,7 +195,7 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
 #pragma unroll
             for (int k = 0; k < CG; ++k) {
                 const int it = ptid + k * kProd;  // (row, c, octet): octet fastest
-                const int oct = it & 3, c = (it >> 2) % CT, row = (it >> 2) / CT;
+                const int oct = it & 3, c = item_row((it >> 2) % CT), row = (it >> 2) / CT;
                 const int i = I0 + row, hin = hin0 + i;
                 const int col0 = 2 * (ow0 + 8 * oct) - 4;
                 const bool ok = row < NROWS && i < need && (unsigned)hin < (unsigned)a.H &&
@@ -200,7 +213,7 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
 #pragma unroll
             for (int k = 0; k < CG; ++k) {
                 const int it = ptid + k * kProd;
-                const int oct = it & 3, c = (it >> 2) % CT, row = (it >> 2) / CT;
+                const int oct = it & 3, c = item_row((it >> 2) % CT), row = (it >> 2) / CT;
                 const int i = I0 + row;
                 // Rows past the strip are written too (as zeros: their loads
                 // read 0), so every ring row a step reads holds finite values.
