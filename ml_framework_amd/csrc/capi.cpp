@@ -173,11 +173,8 @@ int conv2d_bwd_impl(const float* Wt, const float* X, const float* dY, float* dX,
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_bwd: kernel larger than padded input");
     SEERA_TRY(check_ptrs(true, Wt, dW, batch > 0 ? X : dW, batch > 0 ? dY : dW,
                          batch > 0 ? dX : dW));
-    const int Ho = conv_out(H, padh, R, strideh), Wo = conv_out(W_in, padw, S, stridew);
-    SEERA_TRY(conv_dgrad(dY, Wt, dX, batch, N, Ho, Wo, C, H, W_in, R, S, strideh, stridew, padh,
-                         padw, st));
-    return conv_wgrad(dY, X, dW, nullptr, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw,
-                      st);
+    return conv_bwd(dY, Wt, X, dX, dW, nullptr, batch, C, H, W_in, N, R, S, strideh, stridew, padh,
+                    padw, st);
 }
 
 int conv2d_bwd_bias_impl(const float* Wt, const float* X, const float* dY, float* dX, float* dW,
@@ -191,10 +188,8 @@ int conv2d_bwd_bias_impl(const float* Wt, const float* X, const float* dY, float
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv2d_bwd: kernel larger than padded input");
     SEERA_TRY(check_ptrs(true, Wt, dW, batch > 0 ? X : dW, batch > 0 ? dY : dW,
                          batch > 0 ? dX : dW));
-    const int Ho = conv_out(H, padh, R, strideh), Wo = conv_out(W_in, padw, S, stridew);
-    SEERA_TRY(conv_dgrad(dY, Wt, dX, batch, N, Ho, Wo, C, H, W_in, R, S, strideh, stridew, padh,
-                         padw, st));
-    return conv_wgrad(dY, X, dW, db, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw, st);
+    return conv_bwd(dY, Wt, X, dX, dW, db, batch, C, H, W_in, N, R, S, strideh, stridew, padh, padw,
+                    st);
 }
 
 int convT_dims(int Hin, int Win, int KH, int KW, int sh, int sw, int ph, int pw, int* Hout,

@@ -385,6 +385,20 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     return run_plan<true>(fill(PixelProblem<1, DgradGather>{}), pl, st);
 }
 
+int conv_bwd(const float* dY, const float* Wconv, const float* X, float* dX, float* dW,
+             float* db, int B, int C, int H, int W, int F, int R, int S, int sh, int sw, int ph,
+             int pw, hipStream_t st) {
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
+    if ((int64_t)B * H * W <= 0x7fffffff && (int64_t)B * Ho * Wo <= 0x7fffffff) {
+        bool fused = false;
+        SEERA_TRY(fused_conv_bwd(dY, Wconv, X, dX, dW, db, B, C, H, W, F, R, S, sh, sw, ph, pw, st,
+                                 &fused));
+        if (fused) return SEERA_OK;
+    }
+    SEERA_TRY(conv_dgrad(dY, Wconv, dX, B, F, Ho, Wo, C, H, W, R, S, sh, sw, ph, pw, st));
+    return conv_wgrad(dY, X, dW, db, B, C, H, W, F, R, S, sh, sw, ph, pw, st);
+}
+
 int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H, int W,
                int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st) {
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;

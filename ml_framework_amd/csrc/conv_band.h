@@ -125,6 +125,20 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
                           int R, int S, int ph, int pw, bool with_db, hipStream_t st,
                           WgradPartials* out, bool* used);
 
+// Sums the partials into dW [F, C, R, S] in a fixed order (and, with dbpart,
+// the bias-gradient partials into db), one launch (conv_band.hip).
+int reduce_wgrad_partials(const float* part, float* dW, int F, int C, int R, int S, int CT,
+                          int nctile, int ntiles, int nsplit, hipStream_t st, const float* dbpart,
+                          float* db);
+
+// Conv2D backward of a 3x3, stride 1, pad 1, 64 -> 64 channel layer in one
+// pass over dY (conv_bwd_fused.hip): dX [B, 64, H, W], dW [64, 64, 3, 3] and,
+// when db is not nullptr, db [64]; runs when W % 4 == 0, W <= 56 and the
+// tensors are 16-byte aligned; *used reports whether it ran.
+int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* dX, float* dW,
+                   float* db, int B, int C, int H, int W, int F, int R, int S, int sh, int sw,
+                   int ph, int pw, hipStream_t st, bool* used);
+
 // Row-streaming dW partials of a 4x4 stride-2 padding-1 convolution
 // (conv_wgrad_s2.hip): Y [B, F, Ho, Wo], X [B, C, H, W]; runs when W and Wo
 // are multiples of 4; *used reports whether it ran. The caller reduces them.

@@ -1037,6 +1037,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+int reduce_wgrad_partials(const float* part, float* dW, int F, int C, int R, int S, int CT,
+                          int nctile, int ntiles, int nsplit, hipStream_t st, const float* dbpart,
+                          float* db) {
+    SEERA_HIP_TRY(launch_wgrad_reduce(part, dW, F, C, R, S, CT, nctile, ntiles, nsplit, st, dbpart,
+                                      db));
+    return SEERA_OK;
+}
+
 int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F,
                   int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used,
                   const ConvEpi& epi) {

@@ -1,0 +1,546 @@
+// conv_bwd_fused.hip -- Conv2D backward (dX, dW and optionally db) of a 3x3,
+// stride 1, pad 1 layer of 64 -> 64 channels in one pass over dY.
+//
+// Both gradients read dY at the same place for an input position (h, w):
+//   dX[b, c, h, w]  = sum_{f, r, s} W[f, c, r, s] * dY[b, f, h + 1 - r, w + 1 - s]
+//   dW[f, c, r, s]  = sum_{b, h, w} dY[b, f, h + 1 - r, w + 1 - s] * X[b, c, h, w]
+//   db[f]           = sum_{b, oh, ow} dY[b, f, oh, ow]
+// (convolution.cu:144-265 dX, convolution.cu:268-366 and 431-452 dW,
+// Seera_Engine.py:42-65 db). A block owns one image and a strip of L rows of
+// X / dX, and walks it two rows per step:
+//   * 4 producer waves stream the dY rows the step adds (rows h-1 .. h+2 of
+//     the step's X rows h, h+1) and the step's two X rows into two rings of
+//     fp16 channel-last pixels (loaded two steps ahead, rounded on the way in);
+//   * 8 consumer waves each compute a quarter of the step's dX tile
+//     (v_mfma_f32_16x16x32_f16: 16 pixels x 32 filters of the dY ring as A,
+//     the flipped weights, resident in LDS, as B), store it, then accumulate
+//     their 32-filter x 16-channel x 9-tap slice of dW with 32 pixels of dY as
+//     A and of X as B. Those fragments want pixels along K, which the
+//     channel-last rings hold across lanes: ds_read_b64_tr_b16 transposes
+//     them on the way out of LDS.
+// HBM sees dY once (plus two halo rows per strip), X once and dX once. Each
+// block writes its 64 x 576 dW partial (and 64 db partials); wgrad_reduce
+// (conv_band.hip) adds them in a fixed order.
+#include "conv_band.h"
+#include "mfma_core.h"
+
+namespace seera {
+namespace {
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+// The transposed-read builtin's operand type: 4 x __fp16 in LDS.
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+
+__device__ __forceinline__ floatx4_t mfma16x16x32(half8 a, half8 b, floatx4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+constexpr int kG = 2;              // X / dX rows per step
+constexpr int kCons = 512;         // 8 consumer waves
+constexpr int kProd = 256;         // 4 producer waves
+constexpr int kNT = kCons + kProd;
+constexpr int kNRY = 2 * kG + 2;   // dY ring rows: the step's kG + 2, the next step's kG
+constexpr int kNRX = 2 * kG;       // X ring rows: the step's kG, the next step's kG
+constexpr int kTaps = 9;
+constexpr int kWHalves = 2 * kTaps * 2048;  // flipped weights: 2 filter chunks x 9 taps x 64 x 32
+constexpr int kItems = 2;          // row items per producer thread per step
+constexpr int kPreW = 6;           // weight pieces (16 B) per thread, prologue
+constexpr int kYPad = 4;           // dY ring pixel = column + 4
+constexpr int kXPad = 8;           // X ring pixel = column + 8
+
+// Weights: the layout of the row-streaming forward kernel (64 rows x four
+// 16-byte chunks per tap, chunk order rotated by (row >> 1) & 3).
+__device__ __forceinline__ int w_off(int row, int chunk) {
+    return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
+}
+
+// Rings: pixel p of a (row, 32-channel plane) holds its 32 channels as four
+// 16-byte chunks in the order chunk ^ ((p >> 1) & 3), the layout of the
+// row-streaming forward kernel's ring. Measured on gfx950, a ds_read_b128 is
+// conflict-free when every 8 consecutive lanes hit 8 distinct 16-byte slots
+// of a 128-byte window, as is a ds_write_b128; the transposed 64-bit reads
+// when each 32-lane half covers the 64 banks once. Here:
+//   * dX A fragments (16 consecutive pixels at one chunk per 16 lanes): any 8
+//     consecutive pixels differ in p mod 8, which fixes both the pixel's half
+//     of the window and its chunk rotation;
+//   * dW fragments (transposed reads of 16 channels = 32 bytes per pixel, 8
+//     consecutive pixels per half-wave): pixels p and p + 4 share a 64-byte
+//     column and differ in rotation bit 1, so they take its two halves;
+//   * producer writes (two column quads x 4 chunks per 8 lanes): odd quads
+//     write their pixel pairs swapped, so the two pixels of a write differ in
+//     bit 0.
+__device__ __forceinline__ int ring_off(int p, int chunk) {
+    return p * 32 + ((chunk ^ ((p >> 1) & 3)) << 3);
+}
+
+__device__ __forceinline__ half4 read_tr(const half_t* p) {
+    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(p)));
+}
+__device__ __forceinline__ half8 cat8(half4 a, half4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+struct FusedArgs {
+    const float* dy;    // [B, 64, H, W]
+    const float* x;     // [B, 64, H, W]
+    const half_t* wk;   // flipped fp16 weights (prep_bwd_weights)
+    float* dx;          // [B, 64, H, W]
+    float* part;        // [nsplit][64 f][576]: column (r*3 + s)*64 + c
+    float* dbpart;      // [nsplit][64] (nullptr: no bias gradient)
+    int B, H, W;
+    int L, nstrip, nsplit;
+    int BCY, BCX;       // ring pixels per (row, plane)
+    int QW;             // column quads per row (W / 4)
+    int64_t lds_bytes;
+};
+
+// wk[((chunk * 9 + t*3 + u) * 64 + c) * 32 + k] = W[32*chunk + k, c, 2 - t, 2 - u]:
+// the 3x3 transposed convolution dX = conv(dY, flip(W)^T) in the layout the
+// kernel copies to LDS as 16-byte pieces.
+__global__ void prep_bwd_weights(const float* __restrict__ W, half_t* __restrict__ wk) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kWHalves) return;
+    const int k = i & 31, c = (i >> 5) & 63, blk = i >> 11;
+    const int tap = blk % kTaps, chunk = blk / kTaps;
+    const int f = chunk * 32 + k, r = 2 - tap / 3, s = 2 - tap % 3;
+    wk[i] = to_half(W[((f * 64 + c) * 3 + r) * 3 + s]);
+}
+
+template <int NKB>
+__global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    const int split = blockIdx.x;
+    const int b = split / a.nstrip, strip = split - b * a.nstrip;
+    const int h0 = strip * a.L;
+    const int Lb = min(a.L, a.H - h0);         // X / dX rows of this strip
+    const int nsteps = (Lb + kG - 1) / kG;
+    const int PY = a.BCY * 32, PX = a.BCX * 32;  // halves per (row, plane)
+    half_t* const wl = smem;
+    half_t* const ry = smem + kWHalves;        // [kNRY][2 planes][BCY px][32 ch]
+    half_t* const rx = ry + kNRY * 2 * PY;     // [kNRX][2 planes][BCX px][32 ch]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool producer = wave >= kCons / 64;
+    const int ptid = tid - kCons;
+    const int HW = a.H * a.W;
+    const uint32_t cstride = (uint32_t)(HW * 4);
+    const rsrc_t ysrc = make_rsrc(a.dy + (int64_t)b * 64 * HW);
+    const rsrc_t xsrc = make_rsrc(a.x + (int64_t)b * 64 * HW);
+    const int row_items = 8 * a.QW;            // items (8 channels x 4 columns) per row
+    const bool db_on = a.dbpart != nullptr;
+
+    // Item `it` of a group of rows: (row rr, plane, 8-channel group cg, column
+    // quad q4), cg fastest. Its 8 loads (one float4 per channel) and its ring
+    // offset for pixel 4*q4 + pad.
+    auto item_load = [&](rsrc_t src, int it, int img_row, bool ok, floatx4 (&v)[8]) {
+        const int cg = it & 3, q4 = (it >> 2) % a.QW, plane = (it >> 2) / a.QW;
+        const uint32_t vo = ok && (unsigned)img_row < (unsigned)a.H
+            ? (uint32_t)((((plane * 32 + cg * 8) * a.H + img_row) * a.W + 4 * q4) * 4) : kBufOOB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = buf_load4s(src, vo, j * cstride);
+    };
+    auto item_store = [&](half_t* ring_row, int P, int pad, int it, const floatx4 (&v)[8]) {
+        const int cg = it & 3, q4 = (it >> 2) % a.QW, plane = (it >> 2) / a.QW;
+        half_t* dst = ring_row + plane * P;
+        const int sw = q4 & 1;  // odd quads write their pixel pairs swapped
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            float col[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) col[j] = sw ? v[j][jj ^ 1] : v[j][jj];
+            *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + pad + (jj ^ sw), cg)) = pack8(col);
+        }
+    };
+    // Bias gradient: the producers sum each dY item of the strip's own rows
+    // (dY rows h0 .. h0 + Lb - 1) per channel, in fp32 before rounding.
+    auto item_sum = [&](const floatx4 (&v)[8], float (&sum)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum[j] += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+    };
+    float dpro[2][8], dloop[8];  // producers: prologue items' and loop items' sums
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { dpro[0][j] = dpro[1][j] = dloop[j] = 0.f; }
+
+    // ---- prologue: dY rows [h0 - 1, h0 + 3) (strip rows j = 0..3) by the
+    // producers, X rows [h0, h0 + 2) by the consumers (requested first: they
+    // come from HBM), then the weights; the ring pixels outside the image
+    // (never written by the producers) are zeroed ----
+    {
+        floatx4 pv[2][8];
+        // producers: dY items it = ptid + 256k over 4 rows; consumers: X items over 2 rows
+        const int npro = producer ? 4 * row_items : 2 * row_items;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int it = (producer ? ptid : tid) + k * (producer ? kProd : kCons);
+            const int rr = it / row_items;
+            const bool ok = it < npro && (producer ? rr <= Lb + 1 : rr < Lb);
+            if (producer) item_load(ysrc, it % row_items, h0 - 1 + rr, ok, pv[k]);
+            else if (k == 0) item_load(xsrc, it % row_items, h0 + rr, ok, pv[k]);
+        }
+        half8 wv[kPreW];
+#pragma unroll
+        for (int k = 0; k < kPreW; ++k) {
+            const int i = k * kNT + tid;
+            if (i < kWHalves / 8) wv[k] = *reinterpret_cast<const half8*>(a.wk + (int64_t)i * 8);
+        }
+        // padding pixels: dY ring [0, kYPad) and [W + kYPad, BCY), X ring
+        // [0, kXPad) and [W + kXPad, BCX), of every (row, plane), 4 chunks each
+        const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int nyp = a.BCY - a.W, nxp = a.BCX - a.W;
+        const int nzy = kNRY * 2 * nyp * 4, nz = nzy + kNRX * 2 * nxp * 4;
+        for (int i = tid; i < nz; i += kNT) {
+            const bool y = i < nzy;
+            const int iz = y ? i : i - nzy, np = y ? nyp : nxp, pad = y ? kYPad : kXPad;
+            const int rest = iz >> 2, pp = rest % np, rp = rest / np;
+            const int px = pp < pad ? pp : a.W + pp;
+            *reinterpret_cast<half8*>((y ? ry + rp * PY : rx + rp * PX) + px * 32 + (iz & 3) * 8) = z8;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kPreW; ++k) {
+            const int i = k * kNT + tid;
+            if (i < kWHalves / 8)
+                *reinterpret_cast<half8*>(wl + (i >> 8) * 2048 + w_off((i & 255) >> 2, i & 3)) = wv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int it = (producer ? ptid : tid) + k * (producer ? kProd : kCons);
+            const int rr = it / row_items;
+            if (producer) {
+                if (it < npro) {
+                    item_store(ry + rr * 2 * PY, PY, kYPad, it % row_items, pv[k]);
+                    if (db_on && rr >= 1 && rr <= Lb) item_sum(pv[k], dpro[k]);
+                }
+            } else if (k == 0 && it < npro) {
+                item_store(rx + rr * 2 * PX, PX, kXPad, it % row_items, pv[k]);
+            }
+        }
+    }
+
+    if (!producer) {
+        // ---- consumers ----
+        const int G = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+        // dW role: filters 32*fh + 16*fg + (0..15) (fg = 0, 1) x channels 16*cw + (0..15).
+        const int fh = wave & 1, cw = wave >> 1;
+        // Transposed-read offsets (halves) within a ring plane for K block 0
+        // (block kb adds kb * 1024: the rotation repeats every 8 pixels).
+        // Lane (G, e, q) addresses pixel 4G + e + 16*rd of the block and
+        // channels 4q .. 4q + 3 of its 16-channel half; read rd hands lane l
+        // those 4 pixels of channel l % 16, so MFMA K slot 8G + j holds pixel
+        // 4G + (j & 3) + 16*(j >> 2) of the block, for dY and X alike.
+        int oy[2][2];  // [fg][read]: dY ring pixel pd (dY column pd - 4)
+        int ox[3][2];  // [s][read]:  X ring pixel pd + 3 + s (X column pd - 5 + s)
+#pragma unroll
+        for (int rd = 0; rd < 2; ++rd) {
+            const int pd = 4 * G + e + 16 * rd;
+#pragma unroll
+            for (int fg = 0; fg < 2; ++fg) oy[fg][rd] = ring_off(pd, 2 * fg + (q >> 1)) + 4 * (q & 1);
+#pragma unroll
+            for (int s = 0; s < 3; ++s)
+                ox[s][rd] = ring_off(pd + 3 + s, 2 * (cw & 1) + (q >> 1)) + 4 * (q & 1);
+        }
+        // dX role: row dr of the step, pixel groups 2*pxh + pg (16 pixels
+        // each) x channel groups 2*chh + cs (16 channels each), with
+        // v_mfma_f32_16x16x32_f16: the A fragment lane holds pixel lane % 16,
+        // the B fragment lane channel lane % 16, each 8 consecutive filters
+        // (16-byte chunk kc = lane / 16 of a 32-filter plane).
+        const int dr = wave >> 2, pxh = (wave >> 1) & 1, chh = wave & 1;
+        const int kc = lane >> 4;
+        int oa[2][3];  // [pg][u]: A fragment offset within a dY plane
+#pragma unroll
+        for (int pg = 0; pg < 2; ++pg)
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                oa[pg][u] = ring_off(32 * pxh + 16 * pg + (lane & 15) + u + kYPad - 1, kc);
+        const int ob = w_off(lane & 15, kc) + 512 * 2 * chh;  // + 512 * cs
+        const rsrc_t dxdst = make_rsrc(a.dx + (int64_t)b * 64 * HW);
+
+        floatx4_t acc[2][3][3];
+#pragma unroll
+        for (int fg = 0; fg < 2; ++fg)
+#pragma unroll
+            for (int r = 0; r < 3; ++r)
+#pragma unroll
+                for (int s = 0; s < 3; ++s) acc[fg][r][s] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+        for (int st = 0; st < nsteps; ++st) {
+            __syncthreads();  // the rows of step st are in the rings
+            const int i0 = st * kG;  // strip-relative X row of the step's first row
+            // The two consumer waves of a SIMD (w and w + 4) run the dX and dW
+            // halves of the step in opposite order, so that one's LDS waits in
+            // the dX half (one read per MFMA) fall under the other's dW MFMAs.
+            auto dx_half = [&]() {
+            // ---- dX: row i0 + dr, 32 pixels x 32 channels ----
+                floatx4_t ad[2][2];
+#pragma unroll
+                for (int pg = 0; pg < 2; ++pg)
+#pragma unroll
+                    for (int cs = 0; cs < 2; ++cs) ad[pg][cs] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+                half8 fa[2][2], fb[2][2];  // [buf][pg], [buf][cs]
+                // K slice kk = (plane, tap): 32 filters of one tap
+                auto rd_set = [&](int kk, int buf) {
+                    const int plane = kk / kTaps, tap = kk % kTaps, t = tap / 3, u = tap % 3;
+                    const int slot = (i0 + dr + t) % kNRY;  // dY strip row j = i + t
+                    const half_t* yp = ry + (slot * 2 + plane) * PY;
+                    const half_t* wp = wl + kk * 2048 + ob;
+#pragma unroll
+                    for (int pg = 0; pg < 2; ++pg)
+                        fa[buf][pg] = *reinterpret_cast<const half8*>(yp + oa[pg][u]);
+#pragma unroll
+                    for (int cs = 0; cs < 2; ++cs)
+                        fb[buf][cs] = *reinterpret_cast<const half8*>(wp + 512 * cs);
+                };
+                rd_set(0, 0);
+#pragma unroll
+                for (int kk = 0; kk < 2 * kTaps; ++kk) {
+                    if (kk + 1 < 2 * kTaps) rd_set(kk + 1, (kk + 1) & 1);
+#pragma unroll
+                    for (int pg = 0; pg < 2; ++pg)
+#pragma unroll
+                        for (int cs = 0; cs < 2; ++cs)
+                            ad[pg][cs] = mfma16x16x32(fa[kk & 1][pg], fb[kk & 1][cs], ad[pg][cs]);
+                }
+                // lane holds pixels 4*kc + (0..3) of group pg at channel lane % 16
+                const int i = i0 + dr;
+                if (i < Lb) {
+                    const int orow = (h0 + i) * a.W;
+#pragma unroll
+                    for (int pg = 0; pg < 2; ++pg) {
+                        const int px = 32 * pxh + 16 * pg + 4 * kc;
+#pragma unroll
+                        for (int cs = 0; cs < 2; ++cs) {
+                            const int c = 16 * (2 * chh + cs) + (lane & 15);
+                            const uint32_t off = px < a.W ? (uint32_t)((c * HW + orow + px) * 4) : kBufOOB;
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                __builtin_bit_cast(uintx4_t, ad[pg][cs]), dxdst, off, 0, 0);
+                        }
+                    }
+                }
+            };
+            auto dw_half = [&]() {
+            // ---- dW: X rows i0, i0 + 1 against dY rows j = i0 .. i0 + 3 ----
+            // One (K block, X row) pair at a time, its three column shifts of X
+            // against the three dY rows it meets (unrolled, the next pair's
+            // fragments are hoisted and the consumers spill).
+#pragma unroll 1
+            for (int q2 = 0; q2 < 2 * NKB; ++q2) {
+                const int kb = q2 >> 1, ii = q2 & 1;
+                const half_t* xp = rx + (((i0 + ii) % kNRX) * 2 + (cw >> 1)) * PX + kb * 1024;
+                half8 xb[3];
+#pragma unroll
+                for (int s = 0; s < 3; ++s)
+                    xb[s] = cat8(read_tr(xp + ox[s][0]), read_tr(xp + ox[s][1]));
+                half8 ya[2][2];  // [buf][fg]
+                // tap r pairs X row i0 + ii with dY row j = i0 + ii + 2 - r
+                auto rd_y = [&](int r, int buf) {
+                    const half_t* yp = ry + (((i0 + ii + 2 - r) % kNRY) * 2 + fh) * PY + kb * 1024;
+#pragma unroll
+                    for (int fg = 0; fg < 2; ++fg)
+                        ya[buf][fg] = cat8(read_tr(yp + oy[fg][0]), read_tr(yp + oy[fg][1]));
+                };
+                rd_y(0, 0);
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    if (r + 1 < 3) rd_y(r + 1, (r + 1) & 1);
+#pragma unroll
+                    for (int s = 0; s < 3; ++s)
+#pragma unroll
+                        for (int fg = 0; fg < 2; ++fg)
+                            acc[fg][r][s] = mfma16x16x32(ya[r & 1][fg], xb[s], acc[fg][r][s]);
+                }
+            }
+            };
+            // (sched_barrier: left free, the scheduler hoists the second
+            // half's independent LDS reads into the first and spills)
+            dx_half();
+            dw_half();
+        }
+        // Partial: part[split][f][(r*3 + s)*64 + c]; lane holds filters
+        // 4*(lane/16) + i of its 16 x 16 tile at channel lane % 16.
+        float* const dst = a.part + (int64_t)split * 64 * 576;
+#pragma unroll
+        for (int fg = 0; fg < 2; ++fg)
+#pragma unroll
+            for (int r = 0; r < 3; ++r)
+#pragma unroll
+                for (int s = 0; s < 3; ++s) {
+                    const int n = (r * 3 + s) * 64 + 16 * cw + (lane & 15);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        dst[(32 * fh + 16 * fg + 4 * G + i) * 576 + n] = acc[fg][r][s][i];
+                }
+    } else {
+        // ---- producers: the rows of step s + 1 into the rings during step s ----
+        // Thread ptid moves dY item ptid (k = 0: strip row j = 2(s+1) + 2 +
+        // rr) and X item ptid (k = 1: strip row i = 2(s+1) + rr) of the rows a
+        // step adds, so each load's buffer resource is wave-uniform. Decoded
+        // once: row rr (2: none), the byte offset of its 8 channels at column
+        // 4*q4 in image row 0, its ring offset (halves, pixel 4*q4 + pad)
+        // within a ring row, its 8-channel group and chunk rotation.
+        floatx4 v[kItems][8];
+        int prr[kItems], poff[kItems], pdst[kItems], pcg[kItems], prq[kItems];
+        constexpr bool pisy[kItems] = {true, false};
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            const int it2 = ptid;
+            prr[k] = it2 < 2 * row_items ? it2 / row_items : 2;
+            const int ir = it2 % row_items;
+            const int cg = ir & 3, q4 = (ir >> 2) % a.QW, plane = (ir >> 2) / a.QW;
+            const int pad = pisy[k] ? kYPad : kXPad;
+            poff[k] = (((plane * 32 + cg * 8) * a.H) * a.W + 4 * q4) * 4;
+            pdst[k] = plane * (pisy[k] ? PY : PX) + (4 * q4 + pad) * 32;
+            pcg[k] = cg;
+            prq[k] = (2 * q4 + pad / 2) & 3;
+        }
+        auto load_step = [&](int sn) {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k) {
+                const int row = pisy[k] ? h0 + 1 + 2 * sn + prr[k] : h0 + 2 * sn + prr[k];
+                const bool ok = prr[k] < 2 && (pisy[k] ? row <= h0 + Lb : row < h0 + Lb) &&
+                                (unsigned)row < (unsigned)a.H;
+                const uint32_t vo = ok ? (uint32_t)(poff[k] + row * a.W * 4) : kBufOOB;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[k][j] = buf_load4s(pisy[k] ? ysrc : xsrc, vo, j * cstride);
+            }
+        };
+        auto store_step = [&](int sn) {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k) {
+                // dY strip row j = 2sn + 2 + rr up to the last step's window
+                // (rows past Lb + 1 are zeros), X strip rows up to 2*nsteps
+                // (rows past the strip are zeros)
+                const int r = 2 * sn + prr[k] + (pisy[k] ? 2 : 0);
+                if (prr[k] < 2 && r < 2 * nsteps + (pisy[k] ? 2 : 0)) {
+                    half_t* dst = (pisy[k] ? ry + (r % kNRY) * 2 * PY : rx + (r % kNRX) * 2 * PX) + pdst[k];
+                    const int sw = prq[k] >> 1;  // odd quads: pixel pairs swapped
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        float col[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) col[j] = sw ? v[k][j][jj ^ 1] : v[k][j][jj];
+                        const int q = jj ^ sw;  // = ring_off(4*q4 + pad + q, cg) - pdst
+                        *reinterpret_cast<half8*>(dst + q * 32 + ((pcg[k] ^ ((prq[k] + (q >> 1)) & 3)) << 3)) =
+                            pack8(col);
+                    }
+                    if (db_on && pisy[k] && r <= Lb) item_sum(v[k], dloop);
+                }
+            }
+        };
+        __syncthreads();  // releases step 0 (the prologue wrote its rows)
+        load_step(1);
+        for (int s = 0; s + 1 < nsteps; ++s) {
+            // ring slots of step s+1's rows held rows only step s-1 read
+            store_step(s + 1);
+            // (left free, the scheduler hoists the next loads above these
+            // stores, doubling the live item registers, and spills)
+            __builtin_amdgcn_sched_barrier(0);
+            load_step(s + 2);
+            __syncthreads();  // releases step s+1
+        }
+    }
+    if (db_on) {
+        // The producers' sums meet in LDS once every consumer is past its
+        // last ring read; item slots [0, 4*row_items) are the prologue's
+        // (dY strip rows j = 0..3), then the loop's 2*row_items.
+        __syncthreads();
+        floatx4* const red = reinterpret_cast<floatx4*>(smem);
+        if (producer) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int it = ptid + k * kProd;
+                if (it < 4 * row_items) {
+                    red[2 * it] = floatx4{dpro[k][0], dpro[k][1], dpro[k][2], dpro[k][3]};
+                    red[2 * it + 1] = floatx4{dpro[k][4], dpro[k][5], dpro[k][6], dpro[k][7]};
+                }
+            }
+            if (ptid < 2 * row_items) {
+                const int slot = 4 * row_items + ptid;
+                red[2 * slot] = floatx4{dloop[0], dloop[1], dloop[2], dloop[3]};
+                red[2 * slot + 1] = floatx4{dloop[4], dloop[5], dloop[6], dloop[7]};
+            }
+        }
+        __syncthreads();
+        if (producer && ptid < 64) {
+            // filter f = 32*plane + 8*cg + j: items (rr, plane, cg, q4) in order
+            const int f = ptid, plane = f >> 5, cg = (f >> 3) & 3, j = f & 7;
+            const float* redf = reinterpret_cast<const float*>(smem);
+            float sum = 0.f;
+            for (int rr = 0; rr < 6; ++rr)
+                for (int q4 = 0; q4 < a.QW; ++q4) {
+                    const int slot = rr * row_items + (plane * a.QW + q4) * 4 + cg;
+                    sum += redf[slot * 8 + j];
+                }
+            a.dbpart[(int64_t)split * 64 + f] = sum;
+        }
+    }
+}
+
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
+}  // namespace
+
+int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* dX, float* dW,
+                   float* db, int B, int C, int H, int W, int F, int R, int S, int sh, int sw,
+                   int ph, int pw, hipStream_t st, bool* used) {
+    *used = false;
+    if (C != 64 || F != 64 || R != 3 || S != 3 || sh != 1 || sw != 1 || ph != 1 || pw != 1)
+        return SEERA_OK;
+    if (B < 1 || H < 1 || W < 4 || W % 4 != 0 || W > 56) return SEERA_OK;
+    if (((reinterpret_cast<uintptr_t>(dY) | reinterpret_cast<uintptr_t>(X) |
+          reinterpret_cast<uintptr_t>(dX)) & 15) != 0)
+        return SEERA_OK;
+    if ((int64_t)64 * H * W * 4 > kMaxTileSpanBytes) return SEERA_OK;
+    FusedArgs a{};
+    a.dy = dY; a.x = X; a.dx = dX;
+    a.B = B; a.H = H; a.W = W;
+    a.QW = W / 4;
+    // K blocks of 32 dY pixels cover ring pixels [0, 32*nkb), i.e. columns
+    // [-4, 32*nkb - 4); the dX fragments reach ring pixel W + 4.
+    const int nkb = (W + 5 + 31) / 32;
+    a.BCY = 32 * nkb;
+    a.BCX = 32 * nkb + kXPad;
+    a.lds_bytes = (int64_t)kWHalves * 2 + (int64_t)kNRY * 2 * a.BCY * 64 + (int64_t)kNRX * 2 * a.BCX * 64;
+    if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
+    // the db reduction reuses the rings: 6 rows of items x 8 floats
+    if ((int64_t)6 * 8 * a.QW * 32 > a.lds_bytes) return SEERA_OK;
+    // Strip length: fewest rounds of one block per CU, each about (steps + 2)
+    // step times.
+    const int ncu = device_cus();
+    double best = 1e30;
+    for (int L = kG; L < H + kG; L += kG) {
+        const int64_t blocks = (int64_t)B * ((H + L - 1) / L);
+        const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + kG - 1) / kG + 2);
+        if (cost < best) { best = cost; a.L = L; }
+    }
+    a.nstrip = (H + a.L - 1) / a.L;
+    a.nsplit = B * a.nstrip;
+    const size_t w_bytes = (size_t)kWHalves * 2;
+    const size_t part_n = (size_t)a.nsplit * 64 * 576, db_n = db ? (size_t)a.nsplit * 64 : 0;
+    void* ws = nullptr;
+    SEERA_TRY(workspace(w_bytes + sizeof(float) * (part_n + db_n), &ws, st));
+    half_t* wk = static_cast<half_t*>(ws);
+    a.wk = wk;
+    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + w_bytes);
+    a.dbpart = db ? a.part + part_n : nullptr;
+    hipLaunchKernelGGL(prep_bwd_weights, dim3(kWHalves / 256), dim3(256), 0, st, Wconv, wk);
+    SEERA_HIP_TRY(hipGetLastError());
+    const void* k = nkb == 1 ? reinterpret_cast<const void*>(fused_bwd_kernel<1>)
+                             : reinterpret_cast<const void*>(fused_bwd_kernel<2>);
+    SEERA_HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)a.lds_bytes));
+    void* args[] = {&a};
+    SEERA_HIP_TRY(hipLaunchKernel(k, dim3(a.nsplit), dim3(kNT), args, (size_t)a.lds_bytes, st));
+    SEERA_TRY(reduce_wgrad_partials(a.part, dW, 64, 64, 3, 3, 64, 1, 1, a.nsplit, st, a.dbpart, db));
+    *used = true;
+    return SEERA_OK;
+}
+
+}  // namespace seera

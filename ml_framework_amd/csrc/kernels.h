@@ -53,6 +53,13 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
 int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H, int W,
                int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st);
 
+// Conv2D backward: dX = conv_dgrad(dY, Wconv), dW (and db when not nullptr) =
+// conv_wgrad(dY, X); one fused pass over dY where it applies (3x3, stride 1,
+// pad 1, 64 -> 64 channels), the two passes otherwise.
+int conv_bwd(const float* dY, const float* Wconv, const float* X, float* dX, float* dW,
+             float* db, int B, int C, int H, int W, int F, int R, int S, int sh, int sw, int ph,
+             int pw, hipStream_t st);
+
 // ---- tensor_ops.hip: the reference's element-wise, activation, softmax,
 // broadcast, unpooling and reduction functions ----
 enum {

@@ -85,6 +85,20 @@ CONV2D_PHASE2 = [
     ("q06", 1, 64, 17, 16, 32, 4, 4, 2, 1),    # odd input height
 ]
 
+# 3x3 s1 p1 64 -> 64 shapes for the fused one-pass backward (not from the
+# reference's tests): one-row and odd heights (a strip whose last step has one
+# row), one column quad, 24-pixel rows (one 32-pixel K block), 28 and 52
+# pixels (two K blocks, an odd quad count), many two-row strips (halo rows
+# shared between blocks).
+CONV2D_FUSED = [
+    ("f01", 1, 64, 1, 56, 64, 3, 3, 1, 1),
+    ("f02", 2, 64, 3, 4, 64, 3, 3, 1, 1),
+    ("f03", 3, 64, 13, 28, 64, 3, 3, 1, 1),
+    ("f04", 2, 64, 20, 52, 64, 3, 3, 1, 1),
+    ("f05", 1, 64, 40, 24, 64, 3, 3, 1, 1),
+    ("f06", 4, 64, 57, 56, 64, 3, 3, 1, 1),
+]
+
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)
 CONVT = [
     ("t01", 2, 4, 4, 4, 8, 3, 3, 1, 0),

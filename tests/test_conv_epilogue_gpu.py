@@ -143,6 +143,7 @@ BWD_BIAS = [
     ("stream1x1", 5, 16, 12, 12, 8, 1, 1, 0),
     ("band_s2", 4, 32, 32, 32, 64, 3, 2, 1),
     ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),
+    ("fused_odd", 3, 64, 13, 28, 64, 3, 1, 1),            # one-pass dX + dW + db, odd rows
 ]
 
 

@@ -12,7 +12,8 @@ from ml_framework_amd import capi
 from oracle import fp16r
 from tests.helpers import (assert_parity, hip_conv_bwd, hip_conv_fwd, hip_convT_bwd,
                            hip_convT_fwd, rel_fro)
-from tests.shapes import CONV2D, CONV2D_EDGE, CONV2D_PHASE2, CONV2D_STREAM, CONVT, CONVT_PHASE2
+from tests.shapes import (CONV2D, CONV2D_EDGE, CONV2D_FUSED, CONV2D_PHASE2, CONV2D_STREAM,
+                          CONVT, CONVT_PHASE2)
 
 pytestmark = pytest.mark.gpu
 S = oracle.seera_cpp
@@ -29,7 +30,7 @@ def _kaiming(r, shape, fan_in):
     return r.uniform(-lim, lim, shape).astype(np.float32)
 
 
-ALL_CONV2D = CONV2D + CONV2D_STREAM + CONV2D_EDGE + CONV2D_PHASE2
+ALL_CONV2D = CONV2D + CONV2D_STREAM + CONV2D_EDGE + CONV2D_PHASE2 + CONV2D_FUSED
 ALL_CONVT = CONVT + CONVT_PHASE2
 
 
