@@ -160,9 +160,9 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) sum[j] += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
     };
-    float dpro[2][8], dloop[8];  // producers: prologue items' and loop items' sums
+    float dsum[8];  // producers: per-channel sums of their dY items (prologue and loop)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) { dpro[0][j] = dpro[1][j] = dloop[j] = 0.f; }
+    for (int j = 0; j < 8; ++j) dsum[j] = 0.f;
 
     // ---- prologue: dY rows [h0 - 1, h0 + 3) (strip rows j = 0..3) by the
     // producers, X rows [h0, h0 + 2) by the consumers (requested first: they
@@ -170,15 +170,16 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     // (never written by the producers) are zeroed ----
     {
         floatx4 pv[2][8];
-        // producers: dY items it = ptid + 256k over 4 rows; consumers: X items over 2 rows
-        const int npro = producer ? 4 * row_items : 2 * row_items;
+        // producers ptid < 2*row_items: dY items it = ptid + 2*row_items*k of
+        // rows 0..3, the channels of their loop item (so one set of bias
+        // sums serves both); consumers tid < 2*row_items: X item tid of rows 0, 1
+        const bool pro = tid < kCons ? tid < 2 * row_items : ptid < 2 * row_items;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int it = (producer ? ptid : tid) + k * (producer ? kProd : kCons);
+            const int it = (producer ? ptid : tid) + k * 2 * row_items;
             const int rr = it / row_items;
-            const bool ok = it < npro && (producer ? rr <= Lb + 1 : rr < Lb);
-            if (producer) item_load(ysrc, it % row_items, h0 - 1 + rr, ok, pv[k]);
-            else if (k == 0) item_load(xsrc, it % row_items, h0 + rr, ok, pv[k]);
+            if (producer) item_load(ysrc, it % row_items, h0 - 1 + rr, pro && rr <= Lb + 1, pv[k]);
+            else if (k == 0) item_load(xsrc, it % row_items, h0 + rr, pro && rr < Lb, pv[k]);
         }
         half8 wv[kPreW];
 #pragma unroll
@@ -207,14 +208,14 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int it = (producer ? ptid : tid) + k * (producer ? kProd : kCons);
+            const int it = (producer ? ptid : tid) + k * 2 * row_items;
             const int rr = it / row_items;
             if (producer) {
-                if (it < npro) {
+                if (pro) {
                     item_store(ry + rr * 2 * PY, PY, kYPad, it % row_items, pv[k]);
-                    if (db_on && rr >= 1 && rr <= Lb) item_sum(pv[k], dpro[k]);
+                    if (db_on && rr >= 1 && rr <= Lb) item_sum(pv[k], dsum);
                 }
-            } else if (k == 0 && it < npro) {
+            } else if (k == 0 && pro) {
                 item_store(rx + rr * 2 * PX, PX, kXPad, it % row_items, pv[k]);
             }
         }
@@ -231,16 +232,16 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         // channels 4q .. 4q + 3 of its 16-channel half; read rd hands lane l
         // those 4 pixels of channel l % 16, so MFMA K slot 8G + j holds pixel
         // 4G + (j & 3) + 16*(j >> 2) of the block, for dY and X alike.
-        int oy[2][2];  // [fg][read]: dY ring pixel pd (dY column pd - 4)
-        int ox[3][2];  // [s][read]:  X ring pixel pd + 3 + s (X column pd - 5 + s)
+        // (read 1 is 16 pixels = 512 halves further, same rotation)
+        int oy[2];  // [fg]: dY ring pixel pd = 4G + e (dY column pd - 4)
+        int ox[3];  // [s]:  X ring pixel pd + 3 + s (X column pd - 5 + s)
+        {
+            const int pd = 4 * G + e;
 #pragma unroll
-        for (int rd = 0; rd < 2; ++rd) {
-            const int pd = 4 * G + e + 16 * rd;
-#pragma unroll
-            for (int fg = 0; fg < 2; ++fg) oy[fg][rd] = ring_off(pd, 2 * fg + (q >> 1)) + 4 * (q & 1);
+            for (int fg = 0; fg < 2; ++fg) oy[fg] = ring_off(pd, 2 * fg + (q >> 1)) + 4 * (q & 1);
 #pragma unroll
             for (int s = 0; s < 3; ++s)
-                ox[s][rd] = ring_off(pd + 3 + s, 2 * (cw & 1) + (q >> 1)) + 4 * (q & 1);
+                ox[s] = ring_off(pd + 3 + s, 2 * (cw & 1) + (q >> 1)) + 4 * (q & 1);
         }
         // dX role: row dr of the step, pixel groups 2*pxh + pg (16 pixels
         // each) x channel groups 2*chh + cs (16 channels each), with
@@ -249,12 +250,10 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         // (16-byte chunk kc = lane / 16 of a 32-filter plane).
         const int dr = wave >> 2, pxh = (wave >> 1) & 1, chh = wave & 1;
         const int kc = lane >> 4;
-        int oa[2][3];  // [pg][u]: A fragment offset within a dY plane
+        int oa[3];  // [u]: A fragment offset of pixel group 0 within a dY plane
+                    // (group 1 sits 16 pixels = 512 halves further, same rotation)
 #pragma unroll
-        for (int pg = 0; pg < 2; ++pg)
-#pragma unroll
-            for (int u = 0; u < 3; ++u)
-                oa[pg][u] = ring_off(32 * pxh + 16 * pg + (lane & 15) + u + kYPad - 1, kc);
+        for (int u = 0; u < 3; ++u) oa[u] = ring_off(32 * pxh + (lane & 15) + u + kYPad - 1, kc);
         const int ob = w_off(lane & 15, kc) + 512 * 2 * chh;  // + 512 * cs
         const rsrc_t dxdst = make_rsrc(a.dx + (int64_t)b * 64 * HW);
 
@@ -279,29 +278,35 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
                 for (int pg = 0; pg < 2; ++pg)
 #pragma unroll
                     for (int cs = 0; cs < 2; ++cs) ad[pg][cs] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-                half8 fa[2][2], fb[2][2];  // [buf][pg], [buf][cs]
+                // Three fragment sets in flight: with one, every MFMA group
+                // waits out a full LDS round trip.
+                half8 fa[3][2], fb[3][2];  // [buf][pg], [buf][cs]
                 // K slice kk = (plane, tap): 32 filters of one tap
                 auto rd_set = [&](int kk, int buf) {
                     const int plane = kk / kTaps, tap = kk % kTaps, t = tap / 3, u = tap % 3;
                     const int slot = (i0 + dr + t) % kNRY;  // dY strip row j = i + t
-                    const half_t* yp = ry + (slot * 2 + plane) * PY;
+                    const half_t* yp = ry + (slot * 2 + plane) * PY + oa[u];
                     const half_t* wp = wl + kk * 2048 + ob;
 #pragma unroll
                     for (int pg = 0; pg < 2; ++pg)
-                        fa[buf][pg] = *reinterpret_cast<const half8*>(yp + oa[pg][u]);
+                        fa[buf][pg] = *reinterpret_cast<const half8*>(yp + 512 * pg);
 #pragma unroll
                     for (int cs = 0; cs < 2; ++cs)
                         fb[buf][cs] = *reinterpret_cast<const half8*>(wp + 512 * cs);
                 };
                 rd_set(0, 0);
+                rd_set(1, 1);
 #pragma unroll
                 for (int kk = 0; kk < 2 * kTaps; ++kk) {
-                    if (kk + 1 < 2 * kTaps) rd_set(kk + 1, (kk + 1) & 1);
+                    if (kk + 2 < 2 * kTaps) rd_set(kk + 2, (kk + 2) % 3);
 #pragma unroll
                     for (int pg = 0; pg < 2; ++pg)
 #pragma unroll
                         for (int cs = 0; cs < 2; ++cs)
-                            ad[pg][cs] = mfma16x16x32(fa[kk & 1][pg], fb[kk & 1][cs], ad[pg][cs]);
+                            ad[pg][cs] = mfma16x16x32(fa[kk % 3][pg], fb[kk % 3][cs], ad[pg][cs]);
+                    // (keeps each chunk's reads ahead of the previous chunks'
+                    // MFMAs; left free, the scheduler sinks them to their use)
+                    __builtin_amdgcn_sched_barrier(0);
                 }
                 // lane holds pixels 4*kc + (0..3) of group pg at channel lane % 16
                 const int i = i0 + dr;
@@ -332,14 +337,14 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
                 half8 xb[3];
 #pragma unroll
                 for (int s = 0; s < 3; ++s)
-                    xb[s] = cat8(read_tr(xp + ox[s][0]), read_tr(xp + ox[s][1]));
+                    xb[s] = cat8(read_tr(xp + ox[s]), read_tr(xp + ox[s] + 512));
                 half8 ya[2][2];  // [buf][fg]
                 // tap r pairs X row i0 + ii with dY row j = i0 + ii + 2 - r
                 auto rd_y = [&](int r, int buf) {
                     const half_t* yp = ry + (((i0 + ii + 2 - r) % kNRY) * 2 + fh) * PY + kb * 1024;
 #pragma unroll
                     for (int fg = 0; fg < 2; ++fg)
-                        ya[buf][fg] = cat8(read_tr(yp + oy[fg][0]), read_tr(yp + oy[fg][1]));
+                        ya[buf][fg] = cat8(read_tr(yp + oy[fg]), read_tr(yp + oy[fg] + 512));
                 };
                 rd_y(0, 0);
 #pragma unroll
@@ -380,87 +385,90 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         // once: row rr (2: none), the byte offset of its 8 channels at column
         // 4*q4 in image row 0, its ring offset (halves, pixel 4*q4 + pad)
         // within a ring row, its 8-channel group and chunk rotation.
-        floatx4 v[kItems][8];
-        int prr[kItems], poff[kItems], pdst[kItems], pcg[kItems], prq[kItems];
+        floatx4 va[kItems][8], vb[kItems][8];  // two steps of items in flight
+        // per item: byte offset poff, and packed: ring offset (bits 0-23),
+        // channel group (24-25), chunk rotation (26-27), row rr (28-29)
+        int poff[kItems], pmeta[kItems];
         constexpr bool pisy[kItems] = {true, false};
 #pragma unroll
         for (int k = 0; k < kItems; ++k) {
             const int it2 = ptid;
-            prr[k] = it2 < 2 * row_items ? it2 / row_items : 2;
+            const int rr = it2 < 2 * row_items ? it2 / row_items : 2;
             const int ir = it2 % row_items;
             const int cg = ir & 3, q4 = (ir >> 2) % a.QW, plane = (ir >> 2) / a.QW;
             const int pad = pisy[k] ? kYPad : kXPad;
             poff[k] = (((plane * 32 + cg * 8) * a.H) * a.W + 4 * q4) * 4;
-            pdst[k] = plane * (pisy[k] ? PY : PX) + (4 * q4 + pad) * 32;
-            pcg[k] = cg;
-            prq[k] = (2 * q4 + pad / 2) & 3;
+            pmeta[k] = (plane * (pisy[k] ? PY : PX) + (4 * q4 + pad) * 32) | (cg << 24) |
+                       (((2 * q4 + pad / 2) & 3) << 26) | (rr << 28);
         }
-        auto load_step = [&](int sn) {
-#pragma unroll
-            for (int k = 0; k < kItems; ++k) {
-                const int row = pisy[k] ? h0 + 1 + 2 * sn + prr[k] : h0 + 2 * sn + prr[k];
-                const bool ok = prr[k] < 2 && (pisy[k] ? row <= h0 + Lb : row < h0 + Lb) &&
+        auto load_item = [&](int sn, int k, floatx4 (&v)[8]) {
+            {
+                const int prr = pmeta[k] >> 28;
+                const int row = pisy[k] ? h0 + 1 + 2 * sn + prr : h0 + 2 * sn + prr;
+                const bool ok = prr < 2 && (pisy[k] ? row <= h0 + Lb : row < h0 + Lb) &&
                                 (unsigned)row < (unsigned)a.H;
                 const uint32_t vo = ok ? (uint32_t)(poff[k] + row * a.W * 4) : kBufOOB;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[k][j] = buf_load4s(pisy[k] ? ysrc : xsrc, vo, j * cstride);
+                for (int j = 0; j < 8; ++j) v[j] = buf_load4s(pisy[k] ? ysrc : xsrc, vo, j * cstride);
             }
         };
-        auto store_step = [&](int sn) {
-#pragma unroll
-            for (int k = 0; k < kItems; ++k) {
+        auto store_item = [&](int sn, int k, const floatx4 (&v)[8]) {
+            {
                 // dY strip row j = 2sn + 2 + rr up to the last step's window
                 // (rows past Lb + 1 are zeros), X strip rows up to 2*nsteps
                 // (rows past the strip are zeros)
-                const int r = 2 * sn + prr[k] + (pisy[k] ? 2 : 0);
-                if (prr[k] < 2 && r < 2 * nsteps + (pisy[k] ? 2 : 0)) {
-                    half_t* dst = (pisy[k] ? ry + (r % kNRY) * 2 * PY : rx + (r % kNRX) * 2 * PX) + pdst[k];
-                    const int sw = prq[k] >> 1;  // odd quads: pixel pairs swapped
+                const int prr = pmeta[k] >> 28, pcg = (pmeta[k] >> 24) & 3, prq = (pmeta[k] >> 26) & 3;
+                const int r = 2 * sn + prr + (pisy[k] ? 2 : 0);
+                if (prr < 2 && r < 2 * nsteps + (pisy[k] ? 2 : 0)) {
+                    half_t* dst = (pisy[k] ? ry + (r % kNRY) * 2 * PY : rx + (r % kNRX) * 2 * PX) +
+                                  (pmeta[k] & 0xFFFFFF);
+                    const int sw = prq >> 1;  // odd quads: pixel pairs swapped
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
                         float col[8];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) col[j] = sw ? v[k][j][jj ^ 1] : v[k][j][jj];
+                        for (int j = 0; j < 8; ++j) col[j] = sw ? v[j][jj ^ 1] : v[j][jj];
                         const int q = jj ^ sw;  // = ring_off(4*q4 + pad + q, cg) - pdst
-                        *reinterpret_cast<half8*>(dst + q * 32 + ((pcg[k] ^ ((prq[k] + (q >> 1)) & 3)) << 3)) =
+                        *reinterpret_cast<half8*>(dst + q * 32 + ((pcg ^ ((prq + (q >> 1)) & 3)) << 3)) =
                             pack8(col);
                     }
-                    if (db_on && pisy[k] && r <= Lb) item_sum(v[k], dloop);
+                    if (db_on && pisy[k] && r <= Lb) item_sum(v, dsum);
                 }
             }
         };
         __syncthreads();  // releases step 0 (the prologue wrote its rows)
-        load_step(1);
-        for (int s = 0; s + 1 < nsteps; ++s) {
-            // ring slots of step s+1's rows held rows only step s-1 read
-            store_step(s + 1);
-            // (left free, the scheduler hoists the next loads above these
-            // stores, doubling the live item registers, and spills)
-            __builtin_amdgcn_sched_barrier(0);
-            load_step(s + 2);
+        // Step s+2's rows are requested before step s+1's are written, item
+        // by item, so each load has a whole step to arrive (the two register
+        // sets alternate; loads past the last step read nothing).
+        auto step = [&](int sn, floatx4 (&vs)[kItems][8], floatx4 (&vl)[kItems][8]) {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k) {
+                load_item(sn + 1, k, vl[k]);
+                // (left free, the scheduler sinks the loads below the stores)
+                __builtin_amdgcn_sched_barrier(0);
+                store_item(sn, k, vs[k]);  // its ring slots held rows only step sn-2 read
+            }
+        };
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) load_item(1, k, va[k]);
+        for (int s = 0; s + 1 < nsteps; s += 2) {
+            step(s + 1, va, vb);
             __syncthreads();  // releases step s+1
+            if (s + 2 >= nsteps) break;
+            step(s + 2, vb, va);
+            __syncthreads();  // releases step s+2
         }
     }
     if (db_on) {
         // The producers' sums meet in LDS once every consumer is past its
-        // last ring read; item slots [0, 4*row_items) are the prologue's
-        // (dY strip rows j = 0..3), then the loop's 2*row_items.
+        // last ring read: thread ptid < 2*row_items holds the sums of in-row
+        // item ptid % row_items over its rows (rr = ptid / row_items, + 2
+        // per step, and the prologue's rows 1..3).
         __syncthreads();
         floatx4* const red = reinterpret_cast<floatx4*>(smem);
-        if (producer) {
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int it = ptid + k * kProd;
-                if (it < 4 * row_items) {
-                    red[2 * it] = floatx4{dpro[k][0], dpro[k][1], dpro[k][2], dpro[k][3]};
-                    red[2 * it + 1] = floatx4{dpro[k][4], dpro[k][5], dpro[k][6], dpro[k][7]};
-                }
-            }
-            if (ptid < 2 * row_items) {
-                const int slot = 4 * row_items + ptid;
-                red[2 * slot] = floatx4{dloop[0], dloop[1], dloop[2], dloop[3]};
-                red[2 * slot + 1] = floatx4{dloop[4], dloop[5], dloop[6], dloop[7]};
-            }
+        if (producer && ptid < 2 * row_items) {
+            red[2 * ptid] = floatx4{dsum[0], dsum[1], dsum[2], dsum[3]};
+            red[2 * ptid + 1] = floatx4{dsum[4], dsum[5], dsum[6], dsum[7]};
         }
         __syncthreads();
         if (producer && ptid < 64) {
@@ -468,7 +476,7 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             const int f = ptid, plane = f >> 5, cg = (f >> 3) & 3, j = f & 7;
             const float* redf = reinterpret_cast<const float*>(smem);
             float sum = 0.f;
-            for (int rr = 0; rr < 6; ++rr)
+            for (int rr = 0; rr < 2; ++rr)
                 for (int q4 = 0; q4 < a.QW; ++q4) {
                     const int slot = rr * row_items + (plane * a.QW + q4) * 4 + cg;
                     sum += redf[slot * 8 + j];
@@ -510,8 +518,8 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     a.BCX = 32 * nkb + kXPad;
     a.lds_bytes = (int64_t)kWHalves * 2 + (int64_t)kNRY * 2 * a.BCY * 64 + (int64_t)kNRX * 2 * a.BCX * 64;
     if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
-    // the db reduction reuses the rings: 6 rows of items x 8 floats
-    if ((int64_t)6 * 8 * a.QW * 32 > a.lds_bytes) return SEERA_OK;
+    // the db reduction reuses the rings: 2 rows of items x 8 floats
+    if ((int64_t)2 * 8 * a.QW * 32 > a.lds_bytes) return SEERA_OK;
     // Strip length: fewest rounds of one block per CU, each about (steps + 2)
     // step times.
     const int ncu = device_cus();
