@@ -299,11 +299,25 @@ def bench_mlp(steps, warmup, stream):
                     acts[li].ptr, ws[li].ptr, grads[li + 1].ptr, grads[li].ptr, dws[li].ptr, 256,
                     dims[li + 1], dims[li], 1, stream.ptr))
 
+    def bwd_fused_db():
+        # bwd_fused with each layer's db taken from its dB GEMM's loads of dC
+        for li in (2, 1, 0):
+            if li > 0:
+                capi.check(lib.seera_hip_matmul_bwd_relu_bias_async(
+                    acts[li].ptr, ws[li].ptr, grads[li + 1].ptr, masks[li - 1].ptr,
+                    grads[li].ptr, dws[li].ptr, dbs[li].ptr, 256, dims[li + 1], dims[li], 1,
+                    stream.ptr))
+            else:
+                capi.check(lib.seera_hip_matmul_bwd_bias_async(
+                    acts[li].ptr, ws[li].ptr, grads[li + 1].ptr, grads[li].ptr, dws[li].ptr,
+                    dbs[li].ptr, 256, dims[li + 1], dims[li], 1, stream.ptr))
+
     ms_plain = timed(fwd_plain, steps, warmup, stream)
     ms_fused = timed(fwd_fused, steps, warmup, stream)
     ms_db = timed(bias_grads, steps, warmup, stream)
     ms_bwd_plain = timed(bwd_plain, steps, warmup, stream)
     ms_bwd_fused = timed(bwd_fused, steps, warmup, stream)
+    ms_bwd_fused_db = timed(bwd_fused_db, steps, warmup, stream)
     # The same step captured once into a HIP graph and replayed: one launch per
     # step instead of one per kernel (the step is launch-bound at this size).
     import ctypes
@@ -320,7 +334,8 @@ def bench_mlp(steps, warmup, stream):
     flops = sum(2 * 256 * i * o * 3 for i, o in zip(dims[:-1], dims[1:]))
     return {"ms_step": ms, "tflops": flops / (ms * 1e-3) / 1e12, "ms_step_graph": ms_graph,
             "ms_fwd_gemms": ms_plain, "ms_fwd_fused_bias_relu": ms_fused, "ms_bias_grads": ms_db,
-            "ms_bwd_gemms": ms_bwd_plain, "ms_bwd_fused_relu_grad": ms_bwd_fused}
+            "ms_bwd_gemms": ms_bwd_plain, "ms_bwd_fused_relu_grad": ms_bwd_fused,
+            "ms_bwd_fused_relu_grad_db": ms_bwd_fused_db}
 
 
 def bench_transpose(steps, warmup, stream):

@@ -99,6 +99,33 @@ int seera_hip_matmul_bwd_async(const float *A, const float *B, const float *dC,
                                float *dA, float *dB, int M, int N, int K,
                                int Nbatch, void *stream);
 
+/* No single counterpart in the reference: the backward of a Dense layer with
+ * its bias gradient, which the reference runs as cuda_matmul_bwd (GEMM.cu:
+ * 164-225) and a separate sum of dY over the batch rows (Reductionsum,
+ * reductionKernels.cu:12-29, called from Seera_Engine.py:43-65). Here
+ * db[n] = sum over the Nbatch*M rows of dC[., n] (db [N]) is taken in fp32
+ * from the dB GEMM's own loads of dC, in a fixed order (bit-reproducible);
+ * dA and dB are bit-identical to seera_hip_matmul_bwd. */
+int seera_hip_matmul_bwd_bias(const float *A, const float *B, const float *dC,
+                              float *dA, float *dB, float *db, int M, int N,
+                              int K, int Nbatch);
+int seera_hip_matmul_bwd_bias_async(const float *A, const float *B,
+                                    const float *dC, float *dA, float *dB,
+                                    float *db, int M, int N, int K, int Nbatch,
+                                    void *stream);
+/* The two above together for a Dense layer whose input came out of a ReLU:
+ * dA = (dC . B^T) * mask as in seera_hip_matmul_bwd_relu, dB and db as in
+ * seera_hip_matmul_bwd_bias (no single counterpart in the reference). */
+int seera_hip_matmul_bwd_relu_bias(const float *A, const float *B,
+                                   const float *dC, const float *mask,
+                                   float *dA, float *dB, float *db, int M,
+                                   int N, int K, int Nbatch);
+int seera_hip_matmul_bwd_relu_bias_async(const float *A, const float *B,
+                                         const float *dC, const float *mask,
+                                         float *dA, float *dB, float *db, int M,
+                                         int N, int K, int Nbatch,
+                                         void *stream);
+
 /* No single counterpart in the reference: the backward of a Dense layer whose
  * input A came out of a ReLU. The reference runs cuda_matmul_bwd, then the
  * ReLU's chain rule on dA -- local_grad * cp with local_grad the ReLU's 0/1

@@ -52,6 +52,10 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_bias_grad_async": ([_vp, _vp, _i, _i, _vp], _i),
     "seera_hip_matmul_bwd": ([_vp] * 5 + [_i] * 4, _i),
     "seera_hip_matmul_bwd_async": ([_vp] * 5 + [_i] * 4 + [_vp], _i),
+    "seera_hip_matmul_bwd_bias": ([_vp] * 6 + [_i] * 4, _i),
+    "seera_hip_matmul_bwd_bias_async": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "seera_hip_matmul_bwd_relu_bias": ([_vp] * 7 + [_i] * 4, _i),
+    "seera_hip_matmul_bwd_relu_bias_async": ([_vp] * 7 + [_i] * 4 + [_vp], _i),
     "seera_hip_matmul_bwd_relu": ([_vp] * 6 + [_i] * 4, _i),
     "seera_hip_matmul_bwd_relu_async": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "seera_hip_transpose_2d": ([_vp, _vp, _i, _i], _i),

@@ -117,6 +117,24 @@ int matmul_bwd_impl(const float* A, const float* B, const float* dC, float* dA, 
         SEERA_TRY(check_ptrs(true, A, B, dC, dA, dB));
     return gemm_bwd(A, B, dC, dA, dB, M, N, K, Nbatch, st);
 }
+// mask: nullptr for seera_hip_matmul_bwd_bias (checked non-null by the ReLU entry).
+int matmul_bwd_bias_impl(const float* A, const float* B, const float* dC, const float* mask,
+                         float* dA, float* dB, float* db, int M, int N, int K, int Nbatch,
+                         hipStream_t st) {
+    if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "matmul_bwd dims must be >= 0");
+    if (prod(M, N, K, Nbatch) > 0 || prod(K, N) > 0)
+        SEERA_TRY(check_ptrs(true, A, B, dC, dA, dB));
+    if (N > 0) SEERA_TRY(check_ptrs(true, db, db, prod(M, Nbatch, N) > 0 ? dC : db));
+    return gemm_bwd_bias(A, B, dC, mask, dA, dB, db, M, N, K, Nbatch, st);
+}
+int matmul_bwd_relu_bias_impl(const float* A, const float* B, const float* dC, const float* mask,
+                              float* dA, float* dB, float* db, int M, int N, int K, int Nbatch,
+                              hipStream_t st) {
+    if (prod(M, K, Nbatch) > 0) SEERA_TRY(check_ptrs(true, mask, mask, mask));
+    return matmul_bwd_bias_impl(A, B, dC, prod(M, K, Nbatch) > 0 ? mask : nullptr, dA, dB, db, M, N,
+                                K, Nbatch, st);
+}
 int matmul_bwd_relu_impl(const float* A, const float* B, const float* dC, const float* mask,
                          float* dA, float* dB, int M, int N, int K, int Nbatch, hipStream_t st) {
     if (!nonneg(M) || !nonneg(N) || !nonneg(K) || !nonneg(Nbatch))
@@ -327,6 +345,41 @@ int seera_hip_matmul_async(const float* A, const float* B, float* C, int M, int 
 }
 int seera_hip_matmul(const float* A, const float* B, float* C, int M, int N, int K, int Nbatch) {
     return guarded([&] { return sync_after(matmul_impl(A, B, C, M, N, K, Nbatch, nullptr)); });
+}
+
+int seera_hip_matmul_bwd_bias(const float* A, const float* B, const float* dC, float* dA, float* dB,
+                              float* db, int M, int N, int K, int Nbatch) {
+    return guarded([&] {
+        return sync_after(
+            matmul_bwd_bias_impl(A, B, dC, nullptr, dA, dB, db, M, N, K, Nbatch, nullptr));
+    });
+}
+
+int seera_hip_matmul_bwd_bias_async(const float* A, const float* B, const float* dC, float* dA,
+                                    float* dB, float* db, int M, int N, int K, int Nbatch,
+                                    void* stream) {
+    return guarded([&] {
+        return queued(matmul_bwd_bias_impl(A, B, dC, nullptr, dA, dB, db, M, N, K, Nbatch,
+                                           as_stream(stream)));
+    });
+}
+
+int seera_hip_matmul_bwd_relu_bias(const float* A, const float* B, const float* dC,
+                                   const float* mask, float* dA, float* dB, float* db, int M,
+                                   int N, int K, int Nbatch) {
+    return guarded([&] {
+        return sync_after(
+            matmul_bwd_relu_bias_impl(A, B, dC, mask, dA, dB, db, M, N, K, Nbatch, nullptr));
+    });
+}
+
+int seera_hip_matmul_bwd_relu_bias_async(const float* A, const float* B, const float* dC,
+                                         const float* mask, float* dA, float* dB, float* db,
+                                         int M, int N, int K, int Nbatch, void* stream) {
+    return guarded([&] {
+        return queued(matmul_bwd_relu_bias_impl(A, B, dC, mask, dA, dB, db, M, N, K, Nbatch,
+                                                as_stream(stream)));
+    });
 }
 
 int seera_hip_matmul_bwd_relu(const float* A, const float* B, const float* dC, const float* mask,

@@ -26,12 +26,66 @@ struct Operand {
                                              StageMNC<ROWS, BK, NT, VEC>>::type;
 };
 
+// B stagers that also sum, per column, the fp32 values they round into LDS
+// (the bias gradient fused into the dB GEMM, db[n] = sum_k dC[k, n]). A
+// thread's items all sit in the 4-column group (tid % CG) * 4 of the tile, so
+// it keeps 4 sums; values outside the tile or past K load as 0. Only the
+// blocks of row tile 0 count (colsum_begin(true)).
+template <int ROWS, int BK, int NT, int VEC>
+struct ColSumMNC : StageMNC<ROWS, BK, NT, VEC> {
+    using Base = StageMNC<ROWS, BK, NT, VEC>;
+    static_assert(NT % Base::CG == 0, "each thread keeps one 4-column group");
+    float cs[4];
+    bool on;
+    __device__ __forceinline__ void colsum_begin(bool count) {
+        on = count;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cs[q] = 0.f;
+    }
+    __device__ __forceinline__ void store(half_t* tile, int tid) {
+        if (on) {
+#pragma unroll
+            for (int p = 0; p < Base::PASSES; ++p)
+#pragma unroll
+                for (int j = 0; j < Base::KK; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) cs[q] += this->v[p][j][q];
+        }
+        Base::store(tile, tid);
+    }
+};
+
+template <int ROWS, int BK, int NP>
+struct ColSumWsMNC : WsStageMNC<ROWS, BK, NP> {
+    using Base = WsStageMNC<ROWS, BK, NP>;
+    float cs[4];
+    bool on;
+    __device__ __forceinline__ void colsum_begin(bool count) {
+        on = count;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cs[q] = 0.f;
+    }
+    __device__ __forceinline__ void store(const typename Base::Regs& r, int part, half_t* tile,
+                                          int tid) {
+        if (on) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cs[q] += r.v[part][j][q];
+        }
+        Base::store(r, part, tile, tid);
+    }
+};
+
 // EPI: the fused forward epilogue (seera_hip_matmul_bias_act) applies
 // C = act(A.B + bias[n]) as each element is stored, and for ReLU also writes
 // mask = (pre-activation > 0); under split-K the partials are stored raw and
 // splitk_reduce_epi applies it after the sum.
-template <bool A_KC, int VA, bool B_KC, int VB, bool EPI = false>
+// COLSUM (B MN-contiguous only): also colsum[z * N + n] = sum over split z's K
+// range of B(n, k), through the ColSum stagers and p.store_colsum.
+template <bool A_KC, int VA, bool B_KC, int VB, bool EPI = false, bool COLSUM = false>
 struct GemmProblem {
+    static_assert(!COLSUM || !B_KC, "column sums are taken by the MN-contiguous B stagers");
     const float* A;
     const float* B;
     float* C;
@@ -42,13 +96,16 @@ struct GemmProblem {
     const float* bias;     // EPI: [N] or nullptr
     float* mask;           // EPI, act == kActRelu: [M, ldc] or nullptr
     int act;               // EPI: kActNone or kActRelu
+    float* colsum;         // COLSUM: [splits][N]
     static constexpr bool kEpi = EPI;
+    static constexpr bool kColSum = COLSUM;
     static constexpr bool kPipe = true;  // StageKC / StageMNC load without branches
 
     template <int R, int BK, int NT>
     using SA = typename Operand<A_KC, VA>::template Stager<R, BK, NT>;
     template <int R, int BK, int NT>
-    using SB = typename Operand<B_KC, VB>::template Stager<R, BK, NT>;
+    using SB = typename std::conditional<COLSUM, ColSumMNC<R, BK, NT, VB>,
+                                         typename Operand<B_KC, VB>::template Stager<R, BK, NT>>::type;
 
     template <class S>
     __device__ __forceinline__ void load_a(S& s, int m0, int k0, int k1, int tid) const {
@@ -63,7 +120,9 @@ struct GemmProblem {
     template <int R, int BK, int NP>
     using WA = typename std::conditional<A_KC, WsStageKC<R, BK, NP>, WsStageMNC<R, BK, NP>>::type;
     template <int R, int BK, int NP>
-    using WB = typename std::conditional<B_KC, WsStageKC<R, BK, NP>, WsStageMNC<R, BK, NP>>::type;
+    using WB = typename std::conditional<
+        COLSUM, ColSumWsMNC<R, BK, NP>,
+        typename std::conditional<B_KC, WsStageKC<R, BK, NP>, WsStageMNC<R, BK, NP>>::type>::type;
     template <class S>
     __device__ __forceinline__ void ws_init_a(S& s, int m0, int tid) const {
         s.init(A, lda, m0, M, tid);
@@ -77,6 +136,9 @@ struct GemmProblem {
     __device__ __forceinline__ void init_a(S&, int, int) const {}
     template <class S>
     __device__ __forceinline__ void init_b(S&, int, int) const {}
+    __device__ __forceinline__ void store_colsum(int n, int z, float v) const {
+        if (n < N) colsum[(int64_t)z * N + n] = v;
+    }
     __device__ __forceinline__ void store(int m, int n, int z, float v) const {
         const int64_t i = z * split_stride + (int64_t)m * ldc + n;
         if constexpr (EPI) {
@@ -105,9 +167,10 @@ struct Epi {
     int act = kActNone;
 };
 
-template <bool A_KC, bool B_KC, bool EPI = false>
+template <bool A_KC, bool B_KC, bool EPI = false, bool COLSUM = false>
 int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
-                  int64_t ldc, int M, int N, int K, hipStream_t st, Epi epi = Epi{}) {
+                  int64_t ldc, int M, int N, int K, hipStream_t st, Epi epi = Epi{},
+                  float* colsum = nullptr) {
     if (M == 0 || N == 0) return SEERA_OK;
     if (K == 0) {
         // Empty contraction: C = 0 (the reference's K loop never runs), then
@@ -145,12 +208,13 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
         prob.lda = lda; prob.ldb = ldb; prob.ldc = ldc;
         prob.split_stride = 0;
         prob.bias = epi.bias; prob.mask = epi.mask; prob.act = epi.act;
+        prob.colsum = colsum;
         return prob;
     };
-    if (va && vb) return run_plan<true>(fill(GemmProblem<A_KC, 4, B_KC, 4, EPI>{}), pl, st);
-    if (va) return run_plan<false>(fill(GemmProblem<A_KC, 4, B_KC, 1, EPI>{}), pl, st);
-    if (vb) return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 4, EPI>{}), pl, st);
-    return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1, EPI>{}), pl, st);
+    if (va && vb) return run_plan<true>(fill(GemmProblem<A_KC, 4, B_KC, 4, EPI, COLSUM>{}), pl, st);
+    if (va) return run_plan<false>(fill(GemmProblem<A_KC, 4, B_KC, 1, EPI, COLSUM>{}), pl, st);
+    if (vb) return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 4, EPI, COLSUM>{}), pl, st);
+    return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1, EPI, COLSUM>{}), pl, st);
 }
 
 // LDS-tiled transposes of `batch` [rows, cols] slices; 64x64 tiles, coalesced
@@ -295,6 +359,28 @@ int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* 
     // dB [K, N] = A^T [K, Mb] . dC [Mb, N]: A^T element (k, m) = A[m*K + k]
     // is M-contiguous in the output row index k.
     return gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st);
+}
+
+int gemm_bwd_bias(const float* A, const float* B, const float* dC, const float* mask, float* dA,
+                  float* dB, float* db, int M, int N, int K, int Nbatch, hipStream_t st) {
+    const int64_t Mb = (int64_t)M * Nbatch;
+    if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    if (mask) {
+        Epi e;
+        e.mask = const_cast<float*>(mask);  // read, not written, under kActReluGrad
+        e.act = kActReluGrad;
+        SEERA_TRY((gemm_dispatch<true, true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st, e)));
+    } else {
+        SEERA_TRY((gemm_dispatch<true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st)));
+    }
+    // dB [K, N] = A^T . dC with db[n] = sum_m dC[m, n] taken from the same
+    // loads of dC (the blocks of dB's first row tile count them); with no dB
+    // rows, or no rows of dC, db is its own pass (a sum of nothing is 0).
+    if (K > 0 && Mb > 0 && N > 0)
+        return gemm_dispatch<false, false, false, true>(A, K, dC, N, dB, N, K, N, (int)Mb, st,
+                                                        Epi{}, db);
+    SEERA_TRY((gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st)));
+    return bias_grad(dC, db, (int)Mb, N, st);
 }
 
 int transpose(const float* in, float* out, int batch, int rows, int cols, hipStream_t st) {

@@ -11,6 +11,15 @@
 //   p.M, p.N, p.K, p.tiles_n, p.k_split, p.gm
 // gridDim.x = tiles_m * tiles_n, gridDim.z = number of K splits.
 //
+// A problem with `static constexpr bool kColSum = true` (the dB GEMM of a
+// Dense layer with its bias gradient) also sums its B operand over K, per
+// output column: its B stagers keep fp32 sums of the values they round into
+// LDS (sb.colsum_begin(on), sb.cs[4] for the 4 columns (tid % (BN/4))*4 + q
+// of a thread), the blocks of row tile 0 reduce them in a fixed order at the
+// end (colsum_finish) and hand each column's sum of their K range to
+// p.store_colsum(n, z, v). The pipelined kernel then loads zeros past the
+// last slice instead of re-reading it, so that no slice is counted twice.
+//
 // Pipeline (one barrier per BK slice, two LDS stages): the loads of slice t+1
 // are issued from HBM into registers before the matrix cores start on slice t
 // (held in LDS stage t&1); while the MFMAs of k-step kk run, the LDS fragments
@@ -18,9 +27,40 @@
 // rounded to fp16 and written to the other stage.
 #pragma once
 
+#include <type_traits>
+
 #include "mfma_core.h"
 
 namespace seera {
+
+template <class P, class = void>
+struct has_colsum : std::false_type {};
+template <class P>
+struct has_colsum<P, std::void_t<decltype(P::kColSum)>> : std::bool_constant<P::kColSum> {};
+
+// End of a kColSum block of row tile 0 (every thread of the block calls it):
+// holder threads (hid >= 0, NH of them, thread hid holding columns
+// (hid % (ROWS/4))*4 + q) put their sums in LDS by column group, then the
+// first ROWS threads add the NH / (ROWS/4) groups in order.
+template <int ROWS, int NH, class P>
+__device__ __forceinline__ void colsum_finish(const P& p, const float (&cs)[4], int hid, int n0,
+                                              int z, void* smem) {
+    constexpr int CG = ROWS / 4, G = NH / CG;
+    static_assert(NH % CG == 0, "each holder keeps one 4-column group");
+    float* const red = reinterpret_cast<float*>(smem);
+    __syncthreads();  // every LDS tile read is done
+    if (hid >= 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[(hid / CG) * ROWS + (hid % CG) * 4 + q] = cs[q];
+    }
+    __syncthreads();
+    const int c = threadIdx.x;
+    if (c < ROWS) {
+        float t = 0.f;
+        for (int g = 0; g < G; ++g) t += red[g * ROWS + c];
+        p.store_colsum(n0 + c, z, t);
+    }
+}
 
 template <int BM, int BN, int BK, int WM, int WN>
 struct TileCfg {
@@ -56,6 +96,7 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const P p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    static_assert(!has_colsum<P>::value, "column sums run on the pipelined and warp-specialised kernels");
     typename P::template SA<BM, BK, NT> sa;
     typename P::template SB<BN, BK, NT> sb;
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
@@ -156,14 +197,18 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    constexpr bool CS = has_colsum<P>::value;
+    float csum[4] = {0.f, 0.f, 0.f, 0.f};
     if (nk > 0) {
         typename P::template SA<BM, BK, NT> sa[D];
         typename P::template SB<BN, BK, NT> sb[D];
-        auto kof = [&](int s) { return kbeg + min(s, nk - 1) * BK; };
+        // (column sums: slices past the last load zeros, see the header)
+        auto kof = [&](int s) { return kbeg + (CS ? s : min(s, nk - 1)) * BK; };
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             p.init_a(sa[d], m0, tid);
             p.init_b(sb[d], n0, tid);
+            if constexpr (CS) sb[d].colsum_begin(tm == 0);
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -195,6 +240,15 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
         }
         // Drain the (unused) loads still in flight.
         __builtin_amdgcn_s_waitcnt(0);
+        if constexpr (CS) {
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) csum[q] += sb[d].cs[q];
+        }
+    }
+    if constexpr (CS) {
+        if (tm == 0) colsum_finish<BN, NT>(p, csum, tid, n0, blockIdx.z, smem);
     }
 
     const int z = blockIdx.z;
@@ -298,18 +352,25 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const 
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    constexpr bool CS = has_colsum<P>::value;
     if (tid < NC) {
         ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
+        if constexpr (CS) {
+            const float none[4] = {0.f, 0.f, 0.f, 0.f};
+            if (tm == 0) colsum_finish<BN, NP>(p, none, -1, n0, blockIdx.z, smem);
+        }
         return;
     }
 
     // Producer waves.
-    if (nk == 0) return;
     const int ptid = tid - NC;
+    float csum[4] = {0.f, 0.f, 0.f, 0.f};
+    if (nk > 0) {
     typename P::template SA<BM, BK, NP> sa;
     typename P::template SB<BN, BK, NP> sb;
     p.init_a(sa, m0, ptid);
     p.init_b(sb, n0, ptid);
+    if constexpr (CS) sb.colsum_begin(tm == 0);
     p.load_a(sa, m0, kbeg, kend, ptid);
     p.load_b(sb, n0, kbeg, kend, ptid);
     sa.store(smem, ptid);
@@ -329,6 +390,14 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const 
             p.load_b(sb, n0, k0, kend, ptid);
         }
         __syncthreads();  // releases slice kt+1
+    }
+    if constexpr (CS) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) csum[q] = sb.cs[q];
+    }
+    }
+    if constexpr (CS) {
+        if (tm == 0) colsum_finish<BN, NP>(p, csum, ptid, n0, blockIdx.z, smem);
     }
 }
 
@@ -373,19 +442,26 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws2_kernel(const
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    constexpr bool CS = has_colsum<P>::value;
     if (tid < NC) {
         ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
+        if constexpr (CS) {
+            const float none[4] = {0.f, 0.f, 0.f, 0.f};
+            if (tm == 0) colsum_finish<BN, NP>(p, none, -1, n0, blockIdx.z, smem);
+        }
         return;
     }
-    if (nk == 0) return;
 
     const int ptid = tid - NC;
+    float csum[4] = {0.f, 0.f, 0.f, 0.f};
+    if (nk > 0) {
     using SA = typename P::template WA<BM, BK, NP>;
     using SB = typename P::template WB<BN, BK, NP>;
     SA sa;
     SB sb;
     p.ws_init_a(sa, m0, ptid);
     p.ws_init_b(sb, n0, ptid);
+    if constexpr (CS) sb.colsum_begin(tm == 0);
     typename SA::Regs ra[2];
     typename SB::Regs rb[2];
     auto kof = [&](int s) { return kbeg + min(s, nk - 1) * BK; };
@@ -450,6 +526,14 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws2_kernel(const
 #undef SEERA_WS_FENCE
     // Drain the (unused) loads still in flight before the wave ends.
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (CS) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) csum[q] = sb.cs[q];
+    }
+    }
+    if constexpr (CS) {
+        if (tm == 0) colsum_finish<BN, NP>(p, csum, ptid, n0, blockIdx.z, smem);
+    }
 }
 
 template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>

@@ -18,6 +18,11 @@ int bias_grad(const float* dY, float* db, int rows, int N, hipStream_t st);
 // dA = dC . B^T, dB = A^T . dC over the folded batch.
 int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* dB, int M, int N,
              int K, int Nbatch, hipStream_t st);
+// gemm_bwd plus db[n] = sum over the Nbatch*M rows of dC[., n], taken from the
+// dB GEMM's own loads of dC (fp32, before rounding); with a mask, dA as in
+// gemm_bwd_relu.
+int gemm_bwd_bias(const float* A, const float* B, const float* dC, const float* mask, float* dA,
+                  float* dB, float* db, int M, int N, int K, int Nbatch, hipStream_t st);
 // gemm_bwd with dA = (dC . B^T) * mask (the ReLU backward of A's layer).
 int gemm_bwd_relu(const float* A, const float* B, const float* dC, const float* mask, float* dA,
                   float* dB, int M, int N, int K, int Nbatch, hipStream_t st);

@@ -69,9 +69,21 @@ inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split) {
     return best;
 }
 
-// Deterministic split-K reduction: C[m, n] = sum_z P[z][m][n] in z order.
+// Deterministic split-K reduction: C[m, n] = sum_z P[z][m][n] in z order;
+// blocks from nb_c on add the column sums of a kColSum problem instead,
+// out[n] = sum_z cs[z*N + n] (same launch).
 static __global__ void splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
-                                     int M, int N, int64_t ldc, int splits, int64_t stride) {
+                                     int M, int N, int64_t ldc, int splits, int64_t stride,
+                                     int nb_c, const float* __restrict__ cs,
+                                     float* __restrict__ cs_out) {
+    if ((int)blockIdx.x >= nb_c) {
+        const int n = ((int)blockIdx.x - nb_c) * blockDim.x + threadIdx.x;
+        if (n >= N) return;
+        float s = 0.f;
+        for (int z = 0; z < splits; ++z) s += cs[(int64_t)z * N + n];
+        cs_out[n] = s;
+        return;
+    }
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * N) return;
     float s = 0.f;
@@ -142,18 +154,29 @@ hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
                     if (p.K % 32 == 0) return launch_igemm_ws2<256, 256, 32, 4, 2, 4>(p, splits, st);
                 }
                 return launch_igemm_ws<256, 256, 32, 4, 2, 4>(p, splits, st);
-            case Tile::W: return launch_igemm<64, 256, 32, 1, 4>(p, splits, st);
-            case Tile::M: return launch_igemm<128, 128, 32, 2, 2>(p, splits, st);
+            case Tile::W:
+                if constexpr (!pipe_ok<P>::value) return launch_igemm<64, 256, 32, 1, 4>(p, splits, st);
+                break;
+            case Tile::M:
+                if constexpr (!pipe_ok<P>::value) return launch_igemm<128, 128, 32, 2, 2>(p, splits, st);
+                break;
             default: break;
         }
     }
-    return launch_igemm<64, 64, 32, 2, 2>(p, splits, st);
+    // (problems with pipelined stagers never get here: their W, M and S tiles
+    // returned above)
+    if constexpr (pipe_ok<P>::value)
+        return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
+    else
+        return launch_igemm<64, 64, 32, 2, 2>(p, splits, st);
 }
 
 // Runs problem `p` under plan `pl`. Problems that support split-K expose
 // `C`, `ldc` and `split_stride` and a row-major store; `splittable` says so.
 template <bool BIG, class P>
 int run_plan(P p, const Plan& pl, hipStream_t st) {
+    static_assert(!(has_epi<P>::value && has_colsum<P>::value),
+                  "the split-K reduce with an epilogue carries no column sums");
     p.tiles_n = (p.N + tile_bn(pl.tile) - 1) / tile_bn(pl.tile);
     p.k_split = pl.splits > 1 ? pl.k_split : std::max(p.K, 1);
     p.gm = 4;
@@ -161,12 +184,18 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
         return fail(SEERA_ERR_INVALID_ARGUMENT, "grid too large (%d x %d)", p.M, p.N);
     float* final_c = p.C;
     const int64_t final_ld = p.ldc;
+    float* final_cs = nullptr;
+    if constexpr (has_colsum<P>::value) final_cs = p.colsum;
     if (pl.splits > 1) {
+        // split-K partials of C, then (column sums) one row of N per split
+        const size_t cn = (size_t)pl.splits * p.M * p.N;
+        const size_t csn = has_colsum<P>::value ? (size_t)pl.splits * p.N : 0;
         void* ws = nullptr;
-        SEERA_TRY(workspace(sizeof(float) * (size_t)pl.splits * p.M * p.N, &ws, st));
+        SEERA_TRY(workspace(sizeof(float) * (cn + csn), &ws, st));
         p.C = static_cast<float*>(ws);
         p.ldc = p.N;
         p.split_stride = (int64_t)p.M * p.N;
+        if constexpr (has_colsum<P>::value) p.colsum = p.C + cn;
     }
     hipError_t e = launch_tile<BIG>(p, pl.tile, pl.splits, st);
     if (e != hipSuccess) return fail_hip(e, "igemm launch");
@@ -177,8 +206,16 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
                                st, p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride,
                                p.bias, p.mask, p.act);
         } else {
-            hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                               p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride);
+            const int nb_c = (int)((n + 255) / 256);
+            const float* cs = nullptr;
+            int nb_cs = 0;
+            if constexpr (has_colsum<P>::value) {
+                cs = p.colsum;
+                nb_cs = (p.N + 255) / 256;
+            }
+            hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)(nb_c + nb_cs)), dim3(256), 0, st,
+                               p.C, final_c, p.M, p.N, final_ld, pl.splits, p.split_stride, nb_c,
+                               cs, final_cs);
         }
         SEERA_HIP_TRY(hipGetLastError());
     }

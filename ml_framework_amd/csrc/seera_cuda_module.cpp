@@ -151,6 +151,23 @@ PYBIND11_MODULE(seera_cuda, m) {
                                               dev<float>(dA), dev<float>(dB), M, N, K, Nbatch));
           },
           "dA = (dC @ B^T) * mask, dB = A^T @ dC (GPU ptrs)");
+    m.def("cuda_matmul_bwd_bias",
+          [](uintptr_t A, uintptr_t B, uintptr_t dC, uintptr_t dA, uintptr_t dB, uintptr_t db, int M,
+             int N, int K, int Nbatch) {
+              check(seera_hip_matmul_bwd_bias(dev<const float>(A), dev<const float>(B),
+                                              dev<const float>(dC), dev<float>(dA), dev<float>(dB),
+                                              dev<float>(db), M, N, K, Nbatch));
+          },
+          "dA = dC @ B^T, dB = A^T @ dC and db = column sums of dC from the dB GEMM (GPU ptrs)");
+    m.def("cuda_matmul_bwd_relu_bias",
+          [](uintptr_t A, uintptr_t B, uintptr_t dC, uintptr_t mask, uintptr_t dA, uintptr_t dB,
+             uintptr_t db, int M, int N, int K, int Nbatch) {
+              check(seera_hip_matmul_bwd_relu_bias(dev<const float>(A), dev<const float>(B),
+                                                   dev<const float>(dC), dev<const float>(mask),
+                                                   dev<float>(dA), dev<float>(dB), dev<float>(db), M,
+                                                   N, K, Nbatch));
+          },
+          "cuda_matmul_bwd_relu and db = column sums of dC from the dB GEMM (GPU ptrs)");
     m.def("cuda_bias_grad",
           [](uintptr_t dY, uintptr_t db, int rows, int N) {
               check(seera_hip_bias_grad(dev<const float>(dY), dev<float>(db), rows, N));

@@ -202,6 +202,68 @@ def test_fused_relu_backward_against_oracle(M, K, N, nb):
     assert_parity(db, rdb, "dB")
 
 
+BWD_BIAS_SHAPES = [
+    (64, 784, 128, 1),     # BASELINE config 1 (dB [784, 128], contraction 64)
+    (256, 784, 512, 1),    # MLP cfg3 layers
+    (256, 256, 10, 1),     # N = 10: scalar B loads, a partial column tile
+    (2048, 64, 64, 1),     # dB one tile, contraction 2048: split-K, sums reduced over splits
+    (33, 65, 17, 2),       # odd dims, folded batch
+    (7, 13, 5, 3),
+    (2048, 2048, 2048, 1),  # 256x256 warp-specialised tiles, streaming stagers
+    (1000, 4096, 4096, 1),  # contraction 1000 (not whole 32-slices): the other 256x256 kernel
+    (1, 1, 1, 1),
+    (5, 0, 7, 1),          # K = 0: no dB rows, db from its own pass
+    (0, 4, 6, 1),          # no rows: dB = 0, db = 0
+]
+
+
+@pytest.mark.parametrize("M,K,N,nb", BWD_BIAS_SHAPES)
+@pytest.mark.parametrize("relu", [False, True])
+def test_matmul_bwd_bias(M, K, N, nb, relu):
+    """seera_hip_matmul_bwd_bias (and with a ReLU mask on dA,
+    seera_hip_matmul_bwd_relu_bias): dA and dB bit-identical to
+    seera_hip_matmul_bwd (_relu); db against an fp64 sum of dC over the
+    Nbatch*M rows (the reference's Reductionsum, reductionKernels.cu:12-29),
+    and the same bits on a second call (fixed summation order)."""
+    r = np.random.default_rng(M * 3 + K * 5 + N * 7 + nb)
+    a = r.standard_normal((nb, M, K)).astype(np.float32)
+    b = r.standard_normal((K, N)).astype(np.float32)
+    dc = r.standard_normal((nb, M, N)).astype(np.float32)
+    mask = (r.uniform(0, 1, (nb, M, K)) > 0.4).astype(np.float32)
+    n_a, n_b = max(a.size, 1), max(b.size, 1)
+    z1 = np.zeros(1, np.float32)
+    with DeviceBuffer.from_array(a if a.size else z1) as pa, \
+            DeviceBuffer.from_array(b if b.size else z1) as pb, \
+            DeviceBuffer.from_array(dc if dc.size else z1) as pdc, \
+            DeviceBuffer.from_array(mask if mask.size else z1) as pm, \
+            DeviceBuffer(n_a * 4) as pda, DeviceBuffer(n_b * 4) as pdb, \
+            DeviceBuffer(n_a * 4) as pda2, DeviceBuffer(n_b * 4) as pdb2, \
+            DeviceBuffer(max(N, 1) * 4) as db1, DeviceBuffer(max(N, 1) * 4) as db2:
+        if relu:
+            capi.call("seera_hip_matmul_bwd_relu", pa.ptr, pb.ptr, pdc.ptr, pm.ptr, pda.ptr,
+                      pdb.ptr, M, N, K, nb)
+        else:
+            capi.call("seera_hip_matmul_bwd", pa.ptr, pb.ptr, pdc.ptr, pda.ptr, pdb.ptr, M, N, K,
+                      nb)
+        db1.fill(0x7F)
+        for out in (db1, db2):
+            if relu:
+                capi.call("seera_hip_matmul_bwd_relu_bias", pa.ptr, pb.ptr, pdc.ptr, pm.ptr,
+                          pda2.ptr, pdb2.ptr, out.ptr, M, N, K, nb)
+            else:
+                capi.call("seera_hip_matmul_bwd_bias", pa.ptr, pb.ptr, pdc.ptr, pda2.ptr,
+                          pdb2.ptr, out.ptr, M, N, K, nb)
+        if a.size:
+            assert np.array_equal(_bits(pda2.to_array(a.shape)), _bits(pda.to_array(a.shape)))
+        if b.size:
+            assert np.array_equal(_bits(pdb2.to_array(b.shape)), _bits(pdb.to_array(b.shape)))
+        g1, g2 = db1.to_array((N,)), db2.to_array((N,))
+    assert np.array_equal(_bits(g1), _bits(g2))
+    ref = dc.reshape(-1, N).astype(np.float64).sum(axis=0)
+    bound = 1e-6 * np.abs(dc.reshape(-1, N)).astype(np.float64).sum(axis=0) + 1e-6
+    assert np.all(np.abs(g1 - ref) <= bound), float(np.max(np.abs(g1 - ref) / bound))
+
+
 def test_config1_dense_on_its_own_inputs():
     """BASELINE config 1 on the GPU with its own inputs (seed 0: X ~ N(0,1)
     [64, 784], W Kaiming-uniform(fan_in 784) [784, 128], b = 0, dY ~ N(0,1)
@@ -229,6 +291,12 @@ def test_config1_dense_on_its_own_inputs():
         check(lib.seera_hip_bias_grad(pdy.ptr, pdb.ptr, M, N))
         y, dx, dw, db = (py.to_array((M, N)), pdx.to_array((M, K)), pdw.to_array((K, N)),
                          pdb.to_array((N,)))
+        # the same layer's backward with db from the dB GEMM's pass
+        check(lib.seera_hip_matmul_bwd_bias(px.ptr, pw.ptr, pdy.ptr, pdx.ptr, pdw.ptr, pdb.ptr,
+                                            M, N, K, 1))
+        dx2, dw2, db2 = pdx.to_array((M, K)), pdw.to_array((K, N)), pdb.to_array((N,))
+    assert np.array_equal(_bits(dx2), _bits(dx)) and np.array_equal(_bits(dw2), _bits(dw))
+    assert_parity(db2, dy.astype(np.float64).sum(axis=0), "cfg1 db (fused)", rel=1e-6, mabs=1e-4)
     assert_parity(y, S.matmul(fp16r(x), fp16r(w)) + bias, "cfg1 Y")
     rdx, rdw = S.matmul_bwd(fp16r(x), fp16r(w), fp16r(dy))
     assert_parity(dx, rdx, "cfg1 dX")

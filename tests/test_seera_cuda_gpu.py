@@ -164,6 +164,13 @@ def test_fused_layer_entry_points(sc):
     pdbias = sc.cuda_malloc_f32(32)
     sc.cuda_bias_grad(pdc, pdbias, 64, 32)
     assert np.allclose(sc.to_host_f32(pdbias, (32,)), dc.astype(np.float64).sum(0), atol=1e-4)
+    pdbias2 = sc.cuda_malloc_f32(32)
+    sc.cuda_matmul_bwd_bias(pa, pb, pdc, pda2, pdb2, pdbias2, 64, 32, 48, 1)
+    assert np.array_equal(sc.to_host_f32(pdb2, (48, 32)), sc.to_host_f32(pdb, (48, 32)))
+    assert np.allclose(sc.to_host_f32(pdbias2, (32,)), dc.astype(np.float64).sum(0), atol=1e-4)
+    sc.cuda_matmul_bwd_relu_bias(pa, pb, pdc, pma, pda2, pdb2, pdbias2, 64, 32, 48, 1)
+    assert np.array_equal(sc.to_host_f32(pda2, (64, 48)), sc.to_host_f32(pda, (64, 48)) * mask_a)
+    assert np.allclose(sc.to_host_f32(pdbias2, (32,)), dc.astype(np.float64).sum(0), atol=1e-4)
     x = r.standard_normal((2, 8, 10, 12)).astype(np.float32)
     w = (r.standard_normal((16, 8, 3, 3)) * 0.2).astype(np.float32)
     cb = r.standard_normal(16).astype(np.float32)
