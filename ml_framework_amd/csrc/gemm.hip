@@ -28,13 +28,21 @@ struct Operand {
 
 // B stagers that also sum, per column, the fp32 values they round into LDS
 // (the bias gradient fused into the dB GEMM, db[n] = sum_k dC[k, n]). A
-// thread's items all sit in the 4-column group (tid % CG) * 4 of the tile, so
-// it keeps 4 sums; values outside the tile or past K load as 0. Only the
-// blocks of row tile 0 count (colsum_begin(true)).
+// thread's items all sit in one 4-column group of the tile (col0, its
+// reduction slot among the threads of that group: slot), so it keeps 4 sums;
+// values outside the tile or past K load as 0. Only the blocks of row tile 0
+// count (colsum_begin(true)).
 template <int ROWS, int BK, int NT, int VEC>
 struct ColSumMNC : StageMNC<ROWS, BK, NT, VEC> {
     using Base = StageMNC<ROWS, BK, NT, VEC>;
-    static_assert(NT % Base::CG == 0, "each thread keeps one 4-column group");
+    static_assert(NT % Base::CG == 0 && (!Base::kHalfWaveOrder || NT % (4 * Base::CG) == 0),
+                  "each thread keeps one 4-column group");
+    static __device__ __forceinline__ int col0(int tid) {
+        int dr, dk;
+        Base::item_pos(tid, dr, dk);
+        return dr;
+    }
+    static __device__ __forceinline__ int slot(int tid) { return Base::item_slot(tid); }
     float cs[4];
     bool on;
     __device__ __forceinline__ void colsum_begin(bool count) {
@@ -58,6 +66,8 @@ struct ColSumMNC : StageMNC<ROWS, BK, NT, VEC> {
 template <int ROWS, int BK, int NP>
 struct ColSumWsMNC : WsStageMNC<ROWS, BK, NP> {
     using Base = WsStageMNC<ROWS, BK, NP>;
+    static __device__ __forceinline__ int col0(int tid) { return (tid % Base::CG) * 4; }
+    static __device__ __forceinline__ int slot(int tid) { return tid / Base::CG; }
     float cs[4];
     bool on;
     __device__ __forceinline__ void colsum_begin(bool count) {

@@ -14,8 +14,8 @@
 // A problem with `static constexpr bool kColSum = true` (the dB GEMM of a
 // Dense layer with its bias gradient) also sums its B operand over K, per
 // output column: its B stagers keep fp32 sums of the values they round into
-// LDS (sb.colsum_begin(on), sb.cs[4] for the 4 columns (tid % (BN/4))*4 + q
-// of a thread), the blocks of row tile 0 reduce them in a fixed order at the
+// LDS (sb.colsum_begin(on), sb.cs[4] for the 4 columns SB::col0(tid) + q of
+// a thread), the blocks of row tile 0 reduce them in a fixed order at the
 // end (colsum_finish) and hand each column's sum of their K range to
 // p.store_colsum(n, z, v). The pipelined kernel then loads zeros past the
 // last slice instead of re-reading it, so that no slice is counted twice.
@@ -39,19 +39,20 @@ template <class P>
 struct has_colsum<P, std::void_t<decltype(P::kColSum)>> : std::bool_constant<P::kColSum> {};
 
 // End of a kColSum block of row tile 0 (every thread of the block calls it):
-// holder threads (hid >= 0, NH of them, thread hid holding columns
-// (hid % (ROWS/4))*4 + q) put their sums in LDS by column group, then the
-// first ROWS threads add the NH / (ROWS/4) groups in order.
+// holder threads (NH of them, each with the sums of columns col0 + q and a
+// reduction slot in 0 .. NH/(ROWS/4) - 1 among the holders of that column
+// group; slot -1: not a holder) put their sums in LDS, then the first ROWS
+// threads add the slots in order.
 template <int ROWS, int NH, class P>
-__device__ __forceinline__ void colsum_finish(const P& p, const float (&cs)[4], int hid, int n0,
-                                              int z, void* smem) {
+__device__ __forceinline__ void colsum_finish(const P& p, const float (&cs)[4], int col0, int slot,
+                                              int n0, int z, void* smem) {
     constexpr int CG = ROWS / 4, G = NH / CG;
     static_assert(NH % CG == 0, "each holder keeps one 4-column group");
     float* const red = reinterpret_cast<float*>(smem);
     __syncthreads();  // every LDS tile read is done
-    if (hid >= 0) {
+    if (slot >= 0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) red[(hid / CG) * ROWS + (hid % CG) * 4 + q] = cs[q];
+        for (int q = 0; q < 4; ++q) red[slot * ROWS + col0 + q] = cs[q];
     }
     __syncthreads();
     const int c = threadIdx.x;
@@ -248,7 +249,8 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
         }
     }
     if constexpr (CS) {
-        if (tm == 0) colsum_finish<BN, NT>(p, csum, tid, n0, blockIdx.z, smem);
+        using SBT = typename P::template SB<BN, BK, NT>;
+        if (tm == 0) colsum_finish<BN, NT>(p, csum, SBT::col0(tid), SBT::slot(tid), n0, blockIdx.z, smem);
     }
 
     const int z = blockIdx.z;
@@ -357,7 +359,7 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const 
         ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
         if constexpr (CS) {
             const float none[4] = {0.f, 0.f, 0.f, 0.f};
-            if (tm == 0) colsum_finish<BN, NP>(p, none, -1, n0, blockIdx.z, smem);
+            if (tm == 0) colsum_finish<BN, NP>(p, none, 0, -1, n0, blockIdx.z, smem);
         }
         return;
     }
@@ -397,7 +399,8 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws_kernel(const 
     }
     }
     if constexpr (CS) {
-        if (tm == 0) colsum_finish<BN, NP>(p, csum, ptid, n0, blockIdx.z, smem);
+        using SBT = typename P::template SB<BN, BK, NP>;
+        if (tm == 0) colsum_finish<BN, NP>(p, csum, SBT::col0(ptid), SBT::slot(ptid), n0, blockIdx.z, smem);
     }
 }
 
@@ -447,7 +450,7 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws2_kernel(const
         ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
         if constexpr (CS) {
             const float none[4] = {0.f, 0.f, 0.f, 0.f};
-            if (tm == 0) colsum_finish<BN, NP>(p, none, -1, n0, blockIdx.z, smem);
+            if (tm == 0) colsum_finish<BN, NP>(p, none, 0, -1, n0, blockIdx.z, smem);
         }
         return;
     }
@@ -532,7 +535,8 @@ __global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws2_kernel(const
     }
     }
     if constexpr (CS) {
-        if (tm == 0) colsum_finish<BN, NP>(p, csum, ptid, n0, blockIdx.z, smem);
+        using SBT = typename P::template WB<BN, BK, NP>;
+        if (tm == 0) colsum_finish<BN, NP>(p, csum, SBT::col0(ptid), SBT::slot(ptid), n0, blockIdx.z, smem);
     }
 }
 

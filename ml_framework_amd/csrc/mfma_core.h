@@ -186,14 +186,42 @@ struct StageMNC {
     static constexpr int PASSES = (ITEMS + NT - 1) / NT;
     float v[PASSES][KK][4];
 
+    // Item -> (first row dr, first k dk). With KK = 2 each store is a 4-byte
+    // write per lane, served per 32-lane half; the half's lanes take 8 row
+    // groups x the 4 k pairs of one 16-byte chunk, 32 distinct dwords under
+    // the lds_off swizzle (16 row groups x 2 k pairs, the plain order, put
+    // two lanes on every bank). Otherwise consecutive items take
+    // consecutive row groups.
+    static constexpr bool kHalfWaveOrder = KK == 2 && CG % 8 == 0 && KG % 4 == 0;
+    static __device__ __forceinline__ void item_pos(int item, int& dr, int& dk) {
+        if constexpr (kHalfWaveOrder) {
+            const int rest = item >> 5;
+            dr = ((item & 7) + 8 * (rest % (CG / 8))) * 4;
+            dk = (((item >> 3) & 3) + 4 * (rest / (CG / 8))) * KK;
+        } else {
+            dr = (item % CG) * 4;
+            dk = (item / CG) * KK;
+        }
+    }
+    // The other index of the thread's items (0 .. NT/CG - 1): when a thread
+    // keeps one row group over all passes (NT % CG == 0, and NT % (4 CG) == 0
+    // in the half-wave order), (item_pos row group, item_slot) is a bijection
+    // on the threads.
+    static __device__ __forceinline__ int item_slot(int tid) {
+        if constexpr (kHalfWaveOrder)
+            return ((tid >> 3) & 3) + 4 * ((tid >> 5) / (CG / 8));
+        else
+            return tid / CG;
+    }
+
     __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld,
                                          int r0, int rmax, int k0, int kmax, int tid) {
         const rsrc_t rs = make_rsrc(base + k0 * ld + r0);
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int item = p * NT + tid;
-            const int dr = (item % CG) * 4;
-            const int dk = (item / CG) * KK;
+            int dr, dk;
+            item_pos(item, dr, dk);
             const bool live = ITEMS % NT == 0 || item < ITEMS;
 #pragma unroll
             for (int j = 0; j < KK; ++j) {
@@ -220,8 +248,8 @@ struct StageMNC {
         for (int p = 0; p < PASSES; ++p) {
             const int item = p * NT + tid;
             if (ITEMS % NT == 0 || item < ITEMS) {
-                const int row = (item % CG) * 4;
-                const int dk = (item / CG) * KK;
+                int row, dk;
+                item_pos(item, row, dk);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     if constexpr (KK == 8) {
