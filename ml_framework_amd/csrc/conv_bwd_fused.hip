@@ -47,7 +47,6 @@ constexpr int kNRX = 2 * kG;       // X ring rows: the step's kG, the next step'
 constexpr int kTaps = 9;
 constexpr int kWHalves = 2 * kTaps * 2048;  // flipped weights: 2 filter chunks x 9 taps x 64 x 32
 constexpr int kItems = 2;          // row items per producer thread per step
-constexpr int kPreW = 6;           // weight pieces (16 B) per thread, prologue
 constexpr int kYPad = 4;           // dY ring pixel = column + 4
 constexpr int kXPad = 8;           // X ring pixel = column + 8
 
@@ -86,7 +85,7 @@ __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
 struct FusedArgs {
     const float* dy;    // [B, 64, H, W]
     const float* x;     // [B, 64, H, W]
-    const half_t* wk;   // flipped fp16 weights (prep_bwd_weights)
+    const float* w;     // [64 f, 64 c, 3, 3] conv weights (16-byte aligned)
     float* dx;          // [B, 64, H, W]
     float* part;        // [nsplit][64 f][576]: column (r*3 + s)*64 + c
     float* dbpart;      // [nsplit][64] (nullptr: no bias gradient)
@@ -97,17 +96,16 @@ struct FusedArgs {
     int64_t lds_bytes;
 };
 
-// wk[((chunk * 9 + t*3 + u) * 64 + c) * 32 + k] = W[32*chunk + k, c, 2 - t, 2 - u]:
-// the 3x3 transposed convolution dX = conv(dY, flip(W)^T) in the layout the
-// kernel copies to LDS as 16-byte pieces.
-__global__ void prep_bwd_weights(const float* __restrict__ W, half_t* __restrict__ wk) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= kWHalves) return;
-    const int k = i & 31, c = (i >> 5) & 63, blk = i >> 11;
-    const int tap = blk % kTaps, chunk = blk / kTaps;
-    const int f = chunk * 32 + k, r = 2 - tap / 3, s = 2 - tap % 3;
-    wk[i] = to_half(W[((f * 64 + c) * 3 + r) * 3 + s]);
-}
+// The flipped weights in LDS: wl[(chunk * 9 + t*3 + u) * 2048 + w_off(c, k / 8)
+// + k % 8] = W[32*chunk + k, c, 2 - t, 2 - u] in fp16, the 3x3 transposed
+// convolution dX = conv(dY, flip(W)^T). Every block builds them in its
+// prologue from the fp32 weights (L2-resident after the first blocks), one
+// 32-filter chunk at a time, through a natural-order fp16 copy of the chunk
+// in the ring area.
+constexpr int kWLoads = 64 * 576 / 4 / kNT;     // float4 weight loads per thread (12)
+constexpr int kPieces = kTaps * 4 * 64 / kNT;   // 16-byte pieces per thread per chunk (3)
+static_assert(kWLoads * kNT * 4 == 64 * 576 && kPieces * kNT == kTaps * 4 * 64,
+              "the weight build divides evenly over the block");
 
 template <int NKB>
 __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
@@ -166,8 +164,9 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
 
     // ---- prologue: dY rows [h0 - 1, h0 + 3) (strip rows j = 0..3) by the
     // producers, X rows [h0, h0 + 2) by the consumers (requested first: they
-    // come from HBM), then the weights; the ring pixels outside the image
-    // (never written by the producers) are zeroed ----
+    // come from HBM), then the weights, built in LDS while the rows arrive;
+    // the ring pixels outside the image (never written by the producers) are
+    // zeroed ----
     {
         floatx4 pv[2][8];
         // producers ptid < 2*row_items: dY items it = ptid + 2*row_items*k of
@@ -181,12 +180,45 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             if (producer) item_load(ysrc, it % row_items, h0 - 1 + rr, pro && rr <= Lb + 1, pv[k]);
             else if (k == 0) item_load(xsrc, it % row_items, h0 + rr, pro && rr < Lb, pv[k]);
         }
-        half8 wv[kPreW];
+        // The flipped weights, per 32-filter chunk: the fp32 rows of its
+        // filters (float4 i = k * kNT + tid of the chunk's 18432 floats),
+        // their natural-order fp16 copy (filter fl of the chunk, channel c,
+        // tap r*3 + s at half fl*576 + c*9 + r*3 + s), then piece (tap, k
+        // quad kq, c), c fastest, gathers its 8 filters (a 32-lane half reads
+        // 32 distinct banks: 18-byte pixel stride) and writes them as one
+        // 16-byte chunk (8 consecutive c on 8 distinct slots). The second
+        // chunk's loads fly during the first chunk's gathers.
+        floatx4 wf[kWLoads / 2];
+        auto wload = [&](int ch) {
 #pragma unroll
-        for (int k = 0; k < kPreW; ++k) {
-            const int i = k * kNT + tid;
-            if (i < kWHalves / 8) wv[k] = *reinterpret_cast<const half8*>(a.wk + (int64_t)i * 8);
+            for (int k = 0; k < kWLoads / 2; ++k)
+                wf[k] = *reinterpret_cast<const floatx4*>(a.w + ch * 32 * 576 + 4 * (k * kNT + tid));
+        };
+        half_t* const stg = ry;
+        wload(0);
+        for (int ch = 0; ch < 2; ++ch) {
+            if (ch) __syncthreads();  // chunk 0's pieces are read
+#pragma unroll
+            for (int k = 0; k < kWLoads / 2; ++k) {
+                half4 h;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) h[q] = to_half(wf[k][q]);
+                *reinterpret_cast<half4*>(stg + 4 * (k * kNT + tid)) = h;
+            }
+            __syncthreads();
+            if (ch == 0) wload(1);
+#pragma unroll
+            for (int m = 0; m < kPieces; ++m) {
+                const int pc = m * kNT + tid;
+                const int c = pc & 63, kq = (pc >> 6) & 3, tap = pc >> 8;
+                const half_t* src = stg + 8 * kq * 576 + c * 9 + (kTaps - 1 - tap);
+                half8 h;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) h[j] = src[j * 576];
+                *reinterpret_cast<half8*>(wl + (ch * kTaps + tap) * 2048 + w_off(c, kq)) = h;
+            }
         }
+        __syncthreads();  // the staging copy is read: the rings may be written
         // padding pixels: dY ring [0, kYPad) and [W + kYPad, BCY), X ring
         // [0, kXPad) and [W + kXPad, BCX), of every (row, plane), 4 chunks each
         const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -198,13 +230,6 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             const int rest = iz >> 2, pp = rest % np, rp = rest / np;
             const int px = pp < pad ? pp : a.W + pp;
             *reinterpret_cast<half8*>((y ? ry + rp * PY : rx + rp * PX) + px * 32 + (iz & 3) * 8) = z8;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < kPreW; ++k) {
-            const int i = k * kNT + tid;
-            if (i < kWHalves / 8)
-                *reinterpret_cast<half8*>(wl + (i >> 8) * 2048 + w_off((i & 255) >> 2, i & 3)) = wv[k];
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -486,14 +511,6 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     }
 }
 
-int device_cus() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 }  // namespace
 
 int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* dX, float* dW,
@@ -504,11 +521,11 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
         return SEERA_OK;
     if (B < 1 || H < 1 || W < 4 || W % 4 != 0 || W > 56) return SEERA_OK;
     if (((reinterpret_cast<uintptr_t>(dY) | reinterpret_cast<uintptr_t>(X) |
-          reinterpret_cast<uintptr_t>(dX)) & 15) != 0)
+          reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(Wconv)) & 15) != 0)
         return SEERA_OK;
     if ((int64_t)64 * H * W * 4 > kMaxTileSpanBytes) return SEERA_OK;
     FusedArgs a{};
-    a.dy = dY; a.x = X; a.dx = dX;
+    a.dy = dY; a.x = X; a.dx = dX; a.w = Wconv;
     a.B = B; a.H = H; a.W = W;
     a.QW = W / 4;
     // K blocks of 32 dY pixels cover ring pixels [0, 32*nkb), i.e. columns
@@ -518,8 +535,10 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     a.BCX = 32 * nkb + kXPad;
     a.lds_bytes = (int64_t)kWHalves * 2 + (int64_t)kNRY * 2 * a.BCY * 64 + (int64_t)kNRX * 2 * a.BCX * 64;
     if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
-    // the db reduction reuses the rings: 2 rows of items x 8 floats
+    // the db reduction reuses the rings: 2 rows of items x 8 floats; the
+    // weight build stages one chunk (18432 halves) there
     if ((int64_t)2 * 8 * a.QW * 32 > a.lds_bytes) return SEERA_OK;
+    if ((int64_t)kNRY * 2 * a.BCY * 32 + (int64_t)kNRX * 2 * a.BCX * 32 < 32 * 576) return SEERA_OK;
     // Strip length: fewest rounds of one block per CU, each about (steps + 2)
     // step times.
     const int ncu = device_cus();
@@ -531,16 +550,11 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     }
     a.nstrip = (H + a.L - 1) / a.L;
     a.nsplit = B * a.nstrip;
-    const size_t w_bytes = (size_t)kWHalves * 2;
     const size_t part_n = (size_t)a.nsplit * 64 * 576, db_n = db ? (size_t)a.nsplit * 64 : 0;
     void* ws = nullptr;
-    SEERA_TRY(workspace(w_bytes + sizeof(float) * (part_n + db_n), &ws, st));
-    half_t* wk = static_cast<half_t*>(ws);
-    a.wk = wk;
-    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + w_bytes);
+    SEERA_TRY(workspace(sizeof(float) * (part_n + db_n), &ws, st));
+    a.part = static_cast<float*>(ws);
     a.dbpart = db ? a.part + part_n : nullptr;
-    hipLaunchKernelGGL(prep_bwd_weights, dim3(kWHalves / 256), dim3(256), 0, st, Wconv, wk);
-    SEERA_HIP_TRY(hipGetLastError());
     const void* k = nkb == 1 ? reinterpret_cast<const void*>(fused_bwd_kernel<1>)
                              : reinterpret_cast<const void*>(fused_bwd_kernel<2>);
     SEERA_HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)a.lds_bytes));

@@ -503,14 +503,6 @@ hipError_t launch_pxg(const StreamArgs& a, int nftiles, hipStream_t st) {
     return hipGetLastError();
 }
 
-int device_cus() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 }  // namespace
 
 int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used) {

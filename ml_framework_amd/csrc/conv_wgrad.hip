@@ -411,14 +411,6 @@ hipError_t launch_rr(const WStreamArgs& a, int ntiles, hipStream_t st) {
     return hipLaunchKernel(k, dim3(a.nsplit, ntiles), dim3(kNT), args, (size_t)a.lds_bytes, st);
 }
 
-int device_cus() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 }  // namespace
 
 int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, int W, int F,

@@ -272,4 +272,12 @@ void device_memory_stats(size_t* live_bytes, size_t* cached_bytes) {
     if (cached_bytes) *cached_bytes = g_cached_bytes;
 }
 
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
 }  // namespace seera

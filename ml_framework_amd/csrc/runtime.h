@@ -36,6 +36,9 @@ void clear_error();
 // Growing while `st` is being captured fails with SEERA_ERR_INVALID_ARGUMENT.
 int workspace(size_t bytes, void** out, hipStream_t st);
 
+// Compute units of the current device (256 if the query fails).
+int device_cus();
+
 // While alive, workspace() on this host thread hands out [ptr, ptr + bytes)
 // instead of the library's buffers and fails (naming `owner`) for requests
 // above `bytes`. Used by the entry point that must not allocate.
