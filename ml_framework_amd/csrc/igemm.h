@@ -173,20 +173,45 @@ hipError_t launch_igemm(const P& p, int splits, hipStream_t stream) {
 // the last slice re-read it (never stored), so every iteration issues the
 // same loads and the compiler's vmcnt waits stay exact.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WM, int WN, int D, class P>
-__global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
+// KG > 1 splits the block's K range over KG groups of WM x WN waves (each
+// with its own LDS stages and register sets, contiguous parts of the range):
+// more waves per CU keep more loads in flight for the small tiles, whose
+// block count alone leaves one wave per SIMD. Group g > 0 hands its
+// accumulators to group 0 through LDS at the end, added in group order.
+template <int BM, int BN, int BK, int WM, int WN, int D, int KG>
+struct PipeCfg {
+    using Tile = TileCfg<BM, BN, BK, WM, WN>;
+    static constexpr int NTG = Tile::NT;          // threads per group
+    static constexpr int NT = NTG * KG;
+    static constexpr int STAGE = (BM + BN) * BK;  // halves per LDS stage
+    static constexpr int RED_BYTES = KG > 1 ? NTG * Tile::TM * Tile::TN * 16 * 4 : 0;
+    static constexpr int LDS_BYTES =
+        KG * Tile::LDS_BYTES > RED_BYTES ? KG * Tile::LDS_BYTES : RED_BYTES;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS tile exceeds the 160 KB of a gfx950 CU");
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int D, int KG, class P>
+__global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN>;
+    using PC = PipeCfg<BM, BN, BK, WM, WN, D, KG>;
     constexpr int NT = Cfg::NT, TM = Cfg::TM, TN = Cfg::TN;
     static_assert(D >= 2 && D % 2 == 0, "an even number of sets keeps the LDS stage of j fixed");
-    extern __shared__ __attribute__((aligned(16))) half_t smem[];
-    constexpr int STAGE = (BM + BN) * BK;
+    extern __shared__ __attribute__((aligned(16))) half_t smem_all[];
+    constexpr int STAGE = PC::STAGE;
 
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, p.tiles_n, p.gm, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int kbeg = blockIdx.z * p.k_split;
-    const int kend = min(p.K, kbeg + p.k_split);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT) : 0;
+    const int tid = (int)threadIdx.x - grp * NT, lane = tid & 63, wave = tid >> 6;
+    half_t* const smem = smem_all + grp * 2 * STAGE;
+    // this group's part of the block's K slices
+    const int kb0 = blockIdx.z * p.k_split;
+    const int kb1 = min(p.K, kb0 + p.k_split);
+    const int nk_all = kb1 > kb0 ? (kb1 - kb0 + BK - 1) / BK : 0;
+    const int per = (nk_all + KG - 1) / KG;
+    const int kbeg = kb0 + grp * per * BK;
+    const int kend = min(kb1, kbeg + per * BK);
     const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
 
     floatx16 acc[TM][TN];
@@ -198,13 +223,17 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    // every group runs `per` iterations (the barriers are block-wide); a
+    // group with fewer slices skips the MFMAs of the rest
+    const int nit = KG > 1 ? per : nk;
     constexpr bool CS = has_colsum<P>::value;
     float csum[4] = {0.f, 0.f, 0.f, 0.f};
-    if (nk > 0) {
+    if (nit > 0) {
         typename P::template SA<BM, BK, NT> sa[D];
         typename P::template SB<BN, BK, NT> sb[D];
-        // (column sums: slices past the last load zeros, see the header)
-        auto kof = [&](int s) { return kbeg + (CS ? s : min(s, nk - 1)) * BK; };
+        // (column sums: slices past the last load zeros, see the header; a
+        // group without slices has kend <= kbeg: its loads all read 0)
+        auto kof = [&](int s) { return kbeg + (CS ? s : min(s, max(nk - 1, 0))) * BK; };
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             p.init_a(sa[d], m0, tid);
@@ -225,7 +254,7 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
         // (the MFMAs of iterations past the last slice are skipped): the loop
         // has one entry state, which keeps the waits exact across its back
         // edge.
-        for (int kb = 0; kb < nk; kb += D) {
+        for (int kb = 0; kb < nit; kb += D) {
 #pragma unroll
             for (int j = 0; j < D; ++j) {
                 const int kt = kb + j;  // kb is a multiple of D (even): kt & 1 == j & 1
@@ -249,8 +278,41 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
         }
     }
     if constexpr (CS) {
+        // holders: every thread of every group (group g's slots follow g-1's)
         using SBT = typename P::template SB<BN, BK, NT>;
-        if (tm == 0) colsum_finish<BN, NT>(p, csum, SBT::col0(tid), SBT::slot(tid), n0, blockIdx.z, smem);
+        constexpr int kSlots = NT / (BN / 4);
+        if (tm == 0) {
+            colsum_finish<BN, NT * KG>(p, csum, SBT::col0(tid), grp * kSlots + SBT::slot(tid), n0,
+                                       blockIdx.z, smem_all);
+            if constexpr (KG > 1) __syncthreads();  // the sums are read before LDS is reused
+        }
+    }
+    if constexpr (KG > 1) {
+        // groups 1.. hand their accumulators to group 0, one group at a time
+        // (the stage reads of the last iteration ended at its barrier)
+        float* const red = reinterpret_cast<float*>(smem_all);
+#pragma unroll 1
+        for (int g = 1; g < KG; ++g) {
+            if (grp == g) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) red[((i * TN + j) * 16 + r) * NT + tid] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (grp == 0) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * TN + j) * 16 + r) * NT + tid];
+            }
+            __syncthreads();
+        }
+        if (grp != 0) return;
     }
 
     const int z = blockIdx.z;
@@ -268,19 +330,19 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_pipe_kernel(const P p) {
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int D, class P>
+template <int BM, int BN, int BK, int WM, int WN, int D, class P, int KG = 1>
 hipError_t launch_igemm_pipe(const P& p, int splits, hipStream_t stream) {
-    using Cfg = TileCfg<BM, BN, BK, WM, WN>;
+    using PC = PipeCfg<BM, BN, BK, WM, WN, D, KG>;
     const int tiles_m = (p.M + BM - 1) / BM;
     dim3 grid(tiles_m * p.tiles_n, 1, splits);
-    auto kern = igemm_pipe_kernel<BM, BN, BK, WM, WN, D, P>;
-    if (Cfg::LDS_BYTES > 65536) {
+    auto kern = igemm_pipe_kernel<BM, BN, BK, WM, WN, D, KG, P>;
+    if (PC::LDS_BYTES > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Cfg::LDS_BYTES);
+                                           PC::LDS_BYTES);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), Cfg::LDS_BYTES, stream, p);
+    hipLaunchKernelGGL(kern, grid, dim3(PC::NT), PC::LDS_BYTES, stream, p);
     return hipGetLastError();
 }
 

@@ -29,6 +29,10 @@ constexpr int kBK = 32;      // split-K slice granularity (slice ends are predic
                              // not be a multiple of the tile BK; it is a multiple of 4 floats)
 constexpr int kMaxBK = 32;   // deepest K slice of any tile (tile span checks)
 constexpr int kPipeDepth = 2;  // K slices of loads in flight in igemm_pipe_kernel (4 measured no faster)
+// K per block from which a 64x64 tile runs two groups of 4 waves over the
+// halves of its K range (1024^3: 13.2 -> 11.1 us; four groups: 12.4 us; from
+// 512 on, the MLP's GEMMs ran no faster)
+constexpr int kGroupSplitK = 1024;
 
 inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
 inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
@@ -140,7 +144,11 @@ hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
         switch (t) {
             case Tile::W: return launch_igemm_pipe<64, 256, 32, 1, 4, kPipeDepth>(p, splits, st);
             case Tile::M: return launch_igemm_pipe<128, 128, 32, 2, 2, kPipeDepth>(p, splits, st);
-            case Tile::S: return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
+            case Tile::S:
+                // a long K range: two groups of 4 waves over its halves
+                if (p.k_split >= kGroupSplitK)
+                    return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
+                return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
             default: break;
         }
     }

@@ -148,6 +148,9 @@ MATMUL = [
     (256, 784, 512, 1), (256, 512, 256, 1), (256, 256, 10, 1),
     # Dense 64x784x128
     (64, 784, 128, 1),
+    # not from the reference's tests: 64x64 tiles over a contraction of at
+    # least 1024 (two wave groups, each over half of it), with a K tail
+    (512, 1057, 1000, 1), (1000, 1100, 1000, 1),
 ]
 
 # Testing/test_1.py:309-340 -- (name, N, C, H, W, KH, KW, stride, pad), MaxPool2D
