@@ -211,7 +211,7 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
                     (long long)lda, (long long)ldb);
     const bool va = aligned16(A) && lda % 4 == 0 && (A_KC ? K : M) % 4 == 0;
     const bool vb = aligned16(B) && ldb % 4 == 0 && (B_KC ? K : N) % 4 == 0;
-    const Plan pl = plan_tiles(M, N, K, va && vb && big_ok, true);
+    const Plan pl = plan_tiles(M, N, K, va && vb && big_ok, true, true);
     auto fill = [&](auto prob) {
         prob.A = A; prob.B = B; prob.C = C;
         prob.M = M; prob.N = N; prob.K = K;

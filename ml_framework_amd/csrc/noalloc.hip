@@ -23,7 +23,8 @@
 namespace seera {
 
 // The planner (plan.h) splits K only for the 64x64 tile and only when there
-// are fewer than 128 tiles, each split over at most ceil(256 / tiles) parts:
+// are fewer than 128 tiles, each split over at most ceil(256 / tiles) parts
+// (and more than kMaxGroupSplits: fewer run as wave groups in the block):
 // at most 382 partial tiles of 64 x 64 fp32, 6.3 MB. 8 MiB covers every shape;
 // a request above it (a future plan) fails cleanly in workspace().
 constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;

@@ -22,6 +22,7 @@ struct Plan {
     Tile tile;
     int splits;
     int k_split;
+    int groups = 1;  // wave groups over the K range of a 64x64 block (1, 2 or 4)
 };
 
 constexpr int kNumCUs = 256;
@@ -33,6 +34,10 @@ constexpr int kPipeDepth = 2;  // K slices of loads in flight in igemm_pipe_kern
 // halves of its K range (1024^3: 13.2 -> 11.1 us; four groups: 12.4 us; from
 // 512 on, the MLP's GEMMs ran no faster)
 constexpr int kGroupSplitK = 1024;
+// Largest split-K count that 64x64 tiles replace by wave groups in the block
+// (2 or 4 groups of 4 waves, no partials, no reduce launch): MLP cfg3 step
+// 67.6 -> 58.5 us; replacing up to 8 splits: 59.3 us.
+constexpr int kMaxGroupSplits = 4;
 
 inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
 inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
@@ -45,7 +50,8 @@ inline int64_t tile_count(Tile t, int M, int N) {
 // efficiently each tile shape feeds the matrix cores; lowest wins. The 64x256
 // tile weighs a little more than 128x128: per K slice it stages 320 operand
 // rows against 256, and on equal padded work (2048^3) 128x128 ran 13% faster.
-inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split) {
+inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split,
+                       bool allow_groups = false) {
     Tile cands[4] = {Tile::L, Tile::W, Tile::M, Tile::S};
     const double eff[4] = {1.0, 1.25, 1.2, 1.6};
     Plan best{Tile::S, 1, std::max(K, 1)};
@@ -69,6 +75,15 @@ inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split) {
         ks = (ks + kBK - 1) / kBK * kBK;
         best.splits = (K + ks - 1) / ks;
         best.k_split = ks;
+    }
+    if (allow_groups && best.tile == Tile::S) {
+        if (best.splits > 1 && best.splits <= kMaxGroupSplits) {
+            best.groups = best.splits <= 2 ? 2 : 4;
+            best.splits = 1;
+            best.k_split = std::max(K, 1);
+        } else if (best.splits == 1 && K >= kGroupSplitK) {
+            best.groups = 2;
+        }
     }
     return best;
 }
@@ -131,7 +146,7 @@ template <class P>
 struct pipe_ok<P, std::void_t<decltype(P::kPipe)>> : std::bool_constant<P::kPipe> {};
 
 template <bool BIG, class P>
-hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
+hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t st) {
     if constexpr (ws_stream<P>::value) {
         // The 128x128 tile with warp-specialised producers (two waves per
         // block, two K slices in flight): 2048^3 in 33 us against 44 us on
@@ -145,9 +160,9 @@ hipError_t launch_tile(const P& p, Tile t, int splits, hipStream_t st) {
             case Tile::W: return launch_igemm_pipe<64, 256, 32, 1, 4, kPipeDepth>(p, splits, st);
             case Tile::M: return launch_igemm_pipe<128, 128, 32, 2, 2, kPipeDepth>(p, splits, st);
             case Tile::S:
-                // a long K range: two groups of 4 waves over its halves
-                if (p.k_split >= kGroupSplitK)
-                    return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
+                // groups of 4 waves over parts of the block's K range
+                if (groups >= 4) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 4>(p, splits, st);
+                if (groups == 2) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
                 return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
             default: break;
         }
@@ -205,7 +220,7 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
         p.split_stride = (int64_t)p.M * p.N;
         if constexpr (has_colsum<P>::value) p.colsum = p.C + cn;
     }
-    hipError_t e = launch_tile<BIG>(p, pl.tile, pl.splits, st);
+    hipError_t e = launch_tile<BIG>(p, pl.tile, pl.splits, pl.groups, st);
     if (e != hipSuccess) return fail_hip(e, "igemm launch");
     if (pl.splits > 1) {
         const int64_t n = (int64_t)p.M * p.N;

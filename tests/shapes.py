@@ -151,6 +151,9 @@ MATMUL = [
     # not from the reference's tests: 64x64 tiles over a contraction of at
     # least 1024 (two wave groups, each over half of it), with a K tail
     (512, 1057, 1000, 1), (1000, 1100, 1000, 1),
+    # few tiles: four wave groups in place of split-K, the last group's part
+    # one slice or a K tail
+    (256, 400, 256, 1), (256, 500, 256, 1),
 ]
 
 # Testing/test_1.py:309-340 -- (name, N, C, H, W, KH, KW, stride, pad), MaxPool2D
