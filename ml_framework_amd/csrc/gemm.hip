@@ -227,6 +227,55 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
     return run_plan<false>(fill(GemmProblem<A_KC, 1, B_KC, 1, EPI, COLSUM>{}), pl, st);
 }
 
+// The dA and dB GEMMs of a backward (independent of each other) as one
+// launch when both are small (run_plan_pair); any shape or alignment the
+// paired kernel does not take runs as two gemm_dispatch calls.
+struct GemmArgs {
+    const float* A;
+    int64_t lda;
+    const float* B;
+    int64_t ldb;
+    float* C;
+    int64_t ldc;
+    int M, N, K;
+};
+
+template <bool A1_KC, bool B1_KC, bool EPI1, bool A2_KC, bool B2_KC, bool CS2>
+int gemm_pair(const GemmArgs& g1, Epi e1, const GemmArgs& g2, float* colsum2, hipStream_t st) {
+    auto vec = [](const GemmArgs& g, bool a_kc, bool b_kc) {
+        return aligned16(g.A) && g.lda % 4 == 0 && (a_kc ? g.K : g.M) % 4 == 0 &&
+               aligned16(g.B) && g.ldb % 4 == 0 && (b_kc ? g.K : g.N) % 4 == 0;
+    };
+    auto span_ok = [](const GemmArgs& g, bool a_kc, bool b_kc) {
+        auto span = [](bool kc, int rows, int64_t ld) {
+            return kc ? span_kc(rows, kMaxBK, ld) : span_mnc(rows, kMaxBK, ld);
+        };
+        return span(a_kc, 256, g.lda) < kMaxTileSpanBytes && span(b_kc, 256, g.ldb) < kMaxTileSpanBytes;
+    };
+    const bool pairable = g1.M > 0 && g1.N > 0 && g1.K > 0 && g2.M > 0 && g2.N > 0 && g2.K > 0 &&
+                          vec(g1, A1_KC, B1_KC) && vec(g2, A2_KC, B2_KC) &&
+                          span_ok(g1, A1_KC, B1_KC) && span_ok(g2, A2_KC, B2_KC);
+    if (pairable) {
+        GemmProblem<A1_KC, 4, B1_KC, 4, EPI1> p1{};
+        p1.A = g1.A; p1.B = g1.B; p1.C = g1.C;
+        p1.M = g1.M; p1.N = g1.N; p1.K = g1.K;
+        p1.lda = g1.lda; p1.ldb = g1.ldb; p1.ldc = g1.ldc;
+        p1.bias = e1.bias; p1.mask = e1.mask; p1.act = e1.act;
+        GemmProblem<A2_KC, 4, B2_KC, 4, false, CS2> p2{};
+        p2.A = g2.A; p2.B = g2.B; p2.C = g2.C;
+        p2.M = g2.M; p2.N = g2.N; p2.K = g2.K;
+        p2.lda = g2.lda; p2.ldb = g2.ldb; p2.ldc = g2.ldc;
+        p2.colsum = colsum2;
+        const Plan pl1 = plan_tiles(g1.M, g1.N, g1.K, true, true, true);
+        const Plan pl2 = plan_tiles(g2.M, g2.N, g2.K, true, true, true);
+        return run_plan_pair<true, true>(p1, pl1, p2, pl2, st);
+    }
+    SEERA_TRY((gemm_dispatch<A1_KC, B1_KC, EPI1>(g1.A, g1.lda, g1.B, g1.ldb, g1.C, g1.ldc, g1.M,
+                                                 g1.N, g1.K, st, e1)));
+    return gemm_dispatch<A2_KC, B2_KC, false, CS2>(g2.A, g2.lda, g2.B, g2.ldb, g2.C, g2.ldc, g2.M,
+                                                   g2.N, g2.K, st, Epi{}, colsum2);
+}
+
 // LDS-tiled transposes of `batch` [rows, cols] slices; 64x64 tiles, coalesced
 // reads and writes, +1 padding against bank conflicts. Column tiles are on
 // blockIdx.x; row tiles and slices loop over blockIdx.y / blockIdx.z in steps
@@ -325,8 +374,9 @@ int gemm_bwd_relu(const float* A, const float* B, const float* dC, const float* 
     Epi e;
     e.mask = const_cast<float*>(mask);  // read, not written, under kActReluGrad
     e.act = kActReluGrad;
-    SEERA_TRY((gemm_dispatch<true, true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st, e)));
-    return gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st);
+    return gemm_pair<true, true, true, false, false, false>(
+        GemmArgs{dC, N, B, N, dA, K, (int)Mb, K, N}, e, GemmArgs{A, K, dC, N, dB, N, K, N, (int)Mb},
+        nullptr, st);
 }
 
 // db[n] = sum over rows of dY[row, n]: fixed-order partial sums of the rows a
@@ -365,30 +415,38 @@ int gemm_bwd(const float* A, const float* B, const float* dC, float* dA, float* 
     if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
     // dA [Mb, K] = dC [Mb, N] . B^T : B^T element (k, n) = B[k*N + n] is
     // K-contiguous in the GEMM's contraction index n.
-    SEERA_TRY((gemm_dispatch<true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st)));
     // dB [K, N] = A^T [K, Mb] . dC [Mb, N]: A^T element (k, m) = A[m*K + k]
     // is M-contiguous in the output row index k.
-    return gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st);
+    return gemm_pair<true, true, false, false, false, false>(
+        GemmArgs{dC, N, B, N, dA, K, (int)Mb, K, N}, Epi{},
+        GemmArgs{A, K, dC, N, dB, N, K, N, (int)Mb}, nullptr, st);
 }
 
 int gemm_bwd_bias(const float* A, const float* B, const float* dC, const float* mask, float* dA,
                   float* dB, float* db, int M, int N, int K, int Nbatch, hipStream_t st) {
     const int64_t Mb = (int64_t)M * Nbatch;
     if (Mb > 0x7fffffff) return fail(SEERA_ERR_INVALID_ARGUMENT, "Nbatch*M exceeds int range");
+    // dB [K, N] = A^T . dC with db[n] = sum_m dC[m, n] taken from the same
+    // loads of dC (the blocks of dB's first row tile count them); with no dB
+    // rows, or no rows of dC, db is its own pass (a sum of nothing is 0).
+    const GemmArgs ga{dC, N, B, N, dA, K, (int)Mb, K, N}, gb{A, K, dC, N, dB, N, K, N, (int)Mb};
+    if (K > 0 && Mb > 0 && N > 0) {
+        if (mask) {
+            Epi e;
+            e.mask = const_cast<float*>(mask);  // read, not written, under kActReluGrad
+            e.act = kActReluGrad;
+            return gemm_pair<true, true, true, false, false, true>(ga, e, gb, db, st);
+        }
+        return gemm_pair<true, true, false, false, false, true>(ga, Epi{}, gb, db, st);
+    }
     if (mask) {
         Epi e;
-        e.mask = const_cast<float*>(mask);  // read, not written, under kActReluGrad
+        e.mask = const_cast<float*>(mask);
         e.act = kActReluGrad;
         SEERA_TRY((gemm_dispatch<true, true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st, e)));
     } else {
         SEERA_TRY((gemm_dispatch<true, true>(dC, N, B, N, dA, K, (int)Mb, K, N, st)));
     }
-    // dB [K, N] = A^T . dC with db[n] = sum_m dC[m, n] taken from the same
-    // loads of dC (the blocks of dB's first row tile count them); with no dB
-    // rows, or no rows of dC, db is its own pass (a sum of nothing is 0).
-    if (K > 0 && Mb > 0 && N > 0)
-        return gemm_dispatch<false, false, false, true>(A, K, dC, N, dB, N, K, N, (int)Mb, st,
-                                                        Epi{}, db);
     SEERA_TRY((gemm_dispatch<false, false>(A, K, dC, N, dB, N, K, N, (int)Mb, st)));
     return bias_grad(dC, db, (int)Mb, N, st);
 }

@@ -190,23 +190,24 @@ struct PipeCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS tile exceeds the 160 KB of a gfx950 CU");
 };
 
+// Body of igemm_pipe_kernel for block `bid` of `nblk` (split z) of problem p.
 template <int BM, int BN, int BK, int WM, int WN, int D, int KG, class P>
-__global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p) {
+__device__ __forceinline__ void pipe_body(const P& p, int bid, int nblk, int z_split,
+                                          half_t* smem_all) {
     using Cfg = TileCfg<BM, BN, BK, WM, WN>;
     using PC = PipeCfg<BM, BN, BK, WM, WN, D, KG>;
     constexpr int NT = Cfg::NT, TM = Cfg::TM, TN = Cfg::TN;
     static_assert(D >= 2 && D % 2 == 0, "an even number of sets keeps the LDS stage of j fixed");
-    extern __shared__ __attribute__((aligned(16))) half_t smem_all[];
     constexpr int STAGE = PC::STAGE;
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, p.tiles_n, p.gm, tm, tn);
+    tile_coords(bid, nblk, p.tiles_n, p.gm, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT) : 0;
     const int tid = (int)threadIdx.x - grp * NT, lane = tid & 63, wave = tid >> 6;
     half_t* const smem = smem_all + grp * 2 * STAGE;
     // this group's part of the block's K slices
-    const int kb0 = blockIdx.z * p.k_split;
+    const int kb0 = z_split * p.k_split;
     const int kb1 = min(p.K, kb0 + p.k_split);
     const int nk_all = kb1 > kb0 ? (kb1 - kb0 + BK - 1) / BK : 0;
     const int per = (nk_all + KG - 1) / KG;
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p)
         constexpr int kSlots = NT / (BN / 4);
         if (tm == 0) {
             colsum_finish<BN, NT * KG>(p, csum, SBT::col0(tid), grp * kSlots + SBT::slot(tid), n0,
-                                       blockIdx.z, smem_all);
+                                       z_split, smem_all);
             if constexpr (KG > 1) __syncthreads();  // the sums are read before LDS is reused
         }
     }
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p)
         if (grp != 0) return;
     }
 
-    const int z = blockIdx.z;
+    const int z = z_split;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = n0 + wn0 + j * 32 + (lane & 31);
@@ -328,6 +329,26 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p)
                 if (m < p.M) p.store(m, n, z, acc[i][j][r]);
             }
     }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int D, int KG, class P>
+__global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_kernel(const P p) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem_all[];
+    pipe_body<BM, BN, BK, WM, WN, D, KG>(p, blockIdx.x, gridDim.x, blockIdx.z, smem_all);
+}
+
+// Two problems of one tile shape in one launch (the dA and dB GEMMs of a
+// layer's backward, which do not depend on each other): blocks [0, nb1) run
+// p1's tiles, the rest p2's. Neither is split along K.
+template <int BM, int BN, int BK, int WM, int WN, int D, int KG, class P1, class P2>
+__global__ __launch_bounds__(WM* WN * 64 * KG) void igemm_pipe_pair_kernel(const P1 p1, const P2 p2,
+                                                                          int nb1) {
+    extern __shared__ __attribute__((aligned(16))) half_t smem_all[];
+    if ((int)blockIdx.x < nb1)
+        pipe_body<BM, BN, BK, WM, WN, D, KG>(p1, blockIdx.x, nb1, 0, smem_all);
+    else
+        pipe_body<BM, BN, BK, WM, WN, D, KG>(p2, (int)blockIdx.x - nb1, (int)gridDim.x - nb1, 0,
+                                             smem_all);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int D, class P, int KG = 1>

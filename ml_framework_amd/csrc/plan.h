@@ -245,4 +245,41 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
     return SEERA_OK;
 }
 
+template <int KG, class P1, class P2>
+hipError_t launch_igemm_pipe_pair(const P1& p1, int nb1, const P2& p2, int nb2, hipStream_t st) {
+    using PC = PipeCfg<64, 64, 32, 2, 2, kPipeDepth, KG>;
+    auto kern = igemm_pipe_pair_kernel<64, 64, 32, 2, 2, kPipeDepth, KG, P1, P2>;
+    static_assert(PC::LDS_BYTES <= 65536, "the pair kernel's LDS fits the default limit");
+    hipLaunchKernelGGL(kern, dim3((unsigned)(nb1 + nb2)), dim3(PC::NT), PC::LDS_BYTES, st, p1, p2,
+                       nb1);
+    return hipGetLastError();
+}
+
+// Runs two independent problems: in one launch when both plans are unsplit
+// 64x64 pipelined tiles and together fill at most one round of the CUs (the
+// wave-group count of the two plans, the larger one, serves both), else one
+// after the other.
+template <bool BIG1, bool BIG2, class P1, class P2>
+int run_plan_pair(P1 p1, const Plan& pl1, P2 p2, const Plan& pl2, hipStream_t st) {
+    if constexpr (pipe_ok<P1>::value && pipe_ok<P2>::value) {
+        const int64_t nb1 = tile_count(Tile::S, p1.M, p1.N), nb2 = tile_count(Tile::S, p2.M, p2.N);
+        if (pl1.tile == Tile::S && pl2.tile == Tile::S && pl1.splits == 1 && pl2.splits == 1 &&
+            nb1 + nb2 <= kNumCUs) {
+            p1.tiles_n = (p1.N + 63) / 64;
+            p2.tiles_n = (p2.N + 63) / 64;
+            p1.k_split = std::max(p1.K, 1);
+            p2.k_split = std::max(p2.K, 1);
+            p1.gm = p2.gm = 4;
+            const int g = std::max(pl1.groups, pl2.groups);
+            hipError_t e = g >= 4   ? launch_igemm_pipe_pair<4>(p1, (int)nb1, p2, (int)nb2, st)
+                           : g == 2 ? launch_igemm_pipe_pair<2>(p1, (int)nb1, p2, (int)nb2, st)
+                                    : launch_igemm_pipe_pair<1>(p1, (int)nb1, p2, (int)nb2, st);
+            if (e != hipSuccess) return fail_hip(e, "igemm pair launch");
+            return SEERA_OK;
+        }
+    }
+    SEERA_TRY(run_plan<BIG1>(p1, pl1, st));
+    return run_plan<BIG2>(p2, pl2, st);
+}
+
 }  // namespace seera
