@@ -529,6 +529,8 @@ WORKLOADS = {
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,
     "convT_cfg5": bench_convT,
+    "maxpool_2x2_s2": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 2, 2, 0),
+    "maxpool_3x3_s2_p1": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 3, 2, 1),
 }
 
 # Algorithmic HBM bytes of one forward + backward, counted at the API: each

@@ -66,6 +66,7 @@ __device__ __forceinline__ unsigned fdiv(unsigned n, FastDiv f) {
 struct PoolGeom {
     int H, W, R, S, ph, pw, sh, sw, Ho, Wo;
     FastDiv dH, dW, dsh, dsw, dHo, dWo;
+    FastDiv dW4, dWo2;  // W / 4 and Wo / 2 (the 3x3 stride-2 kernels)
 };
 
 // Cell of output index o along one axis: [lo, hi) of the input, clipped.
@@ -298,6 +299,96 @@ __global__ __launch_bounds__(256) void maxpool_bwd_general_t(const float* __rest
     dx[i] = sum;
 }
 
+// 3x3 windows, stride 2, padding 1 (the usual pooling after a stem
+// convolution) with W a multiple of 4: output pair (ho, 2p, 2p + 1) covers
+// input columns 4p - 1 .. 4p + 3 of rows 2ho - 1 .. 2ho + 1, read as one
+// 16-byte load and one 4-byte load per row; each output keeps the general
+// kernel's visit order and tie rule, so the results are the same bits.
+// Wo = W / 2 is even, so the pair is whole.
+__global__ __launch_bounds__(256) void maxpool_fwd_3x3s2p1(const float* __restrict__ x,
+                                                           float* __restrict__ out,
+                                                           int* __restrict__ mask, PoolGeom g,
+                                                           unsigned npairs) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npairs) return;
+    const unsigned t = fdiv(i, g.dWo2), pp = i - t * (unsigned)(g.Wo / 2);
+    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
+    const unsigned plane = bc * (unsigned)(g.H * g.W);
+    const float* xp = x + plane;
+    const int h0 = 2 * (int)ho - 1, c0 = 4 * (int)pp;
+    float v[3][5];
+    bool okr[3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        const int h = h0 + r;
+        okr[r] = h >= 0 && h < g.H;
+        const float* row = xp + h * g.W;
+        const float4 q = okr[r] ? *reinterpret_cast<const float4*>(row + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[r][0] = okr[r] && c0 > 0 ? row[c0 - 1] : 0.f;
+        v[r][1] = q.x; v[r][2] = q.y; v[r][3] = q.z; v[r][4] = q.w;
+    }
+    float best[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int w0 = c0 - 1 + 2 * k;  // window's first column (<= W - 3)
+        float b = okr[0] && w0 >= 0 ? v[0][2 * k] : 0.f;  // the origin, or 0 in the padding
+        int arg = -1;
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int s2 = 0; s2 < 3; ++s2)
+                if (okr[r] && w0 + s2 >= 0 && b <= v[r][2 * k + s2]) {
+                    b = v[r][2 * k + s2];
+                    arg = (h0 + r) * g.W + w0 + s2;
+                }
+        best[k] = b;
+        if (arg >= 0) mask[plane + (unsigned)arg] = 1;
+    }
+    *reinterpret_cast<float2*>(out + (unsigned)(t * g.Wo) + 2 * pp) = make_float2(best[0], best[1]);
+}
+
+// Its backward: one thread per 4 columns 4q .. 4q + 3 of an input row. Row h
+// lies in windows ho = h / 2 .. min(Ho - 1, (h + 1) / 2); column 4q + c in
+// windows wo = 2q + o0[c] .. min(Wo - 1, 2q + o1[c]), o0 = (0, 0, 1, 1),
+// o1 = (0, 1, 1, 2). The terms are added in (ho, wo) order as in the general
+// kernel: the same bits with one 16-byte mask load, 6 dout loads and one
+// 16-byte store per 4 elements.
+__global__ __launch_bounds__(256) void maxpool_bwd_3x3s2p1(const float* __restrict__ dout,
+                                                           const int* __restrict__ mask,
+                                                           float* __restrict__ dx, PoolGeom g,
+                                                           unsigned nquads) {
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nquads) return;
+    const unsigned t = fdiv(i, g.dW4), q = i - t * (unsigned)(g.W / 4);  // t: plane row
+    const unsigned bc = fdiv(t, g.dH);
+    const int h = (int)(t - bc * g.H);
+    const unsigned e = t * (unsigned)g.W + 4 * q;
+    const int4 mk = *reinterpret_cast<const int4*>(mask + e);
+    const float m[4] = {(float)mk.x, (float)mk.y, (float)mk.z, (float)mk.w};
+    const float* gp = dout + bc * (unsigned)(g.Ho * g.Wo);
+    const int ho_lo = h >> 1, ho_hi = min(g.Ho - 1, (h + 1) >> 1);
+    const int wb = 2 * (int)q, wlim = g.Wo - 1;
+    float d[2][3];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            d[a][j] = ho_lo + a <= ho_hi && wb + j <= wlim ? gp[(ho_lo + a) * g.Wo + wb + j] : 0.f;
+    constexpr int o0[4] = {0, 0, 1, 1}, o1[4] = {0, 1, 1, 2};
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float sum = 0.f;
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int j = o0[c]; j <= o1[c]; ++j)
+                if (ho_lo + a <= ho_hi && wb + j <= wlim) sum += d[a][j] * m[c];
+        r[c] = sum;
+    }
+    *reinterpret_cast<float4*>(dx + e) = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 // One thread per input element: the windows covering row h are
 // ho in [ceil((h + ph - R + 1) / sh), floor((h + ph) / sh)] within [0, Ho).
 __global__ __launch_bounds__(256) void maxpool_bwd_general(const float* __restrict__ dout,
@@ -330,7 +421,8 @@ PoolGeom geom(int H, int W, int R, int S, int ph, int pw, int sh, int sw) {
     const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
     return {H, W, R, S, ph, pw, sh, sw, Ho, Wo,
             make_fastdiv(H), make_fastdiv(W), make_fastdiv(sh), make_fastdiv(sw),
-            make_fastdiv(Ho), make_fastdiv(Wo)};
+            make_fastdiv(Ho), make_fastdiv(Wo),
+            make_fastdiv((unsigned)std::max(W / 4, 1)), make_fastdiv((unsigned)std::max(Wo / 2, 1))};
 }
 
 unsigned blocks(unsigned n) { return (n + 255u) / 256u; }
@@ -365,6 +457,12 @@ int launch_bwd_general(const float* dout, const int* mask, float* dx, const Pool
     return SEERA_OK;
 }
 
+bool s2p1_path(int R, int S, int ph, int pw, int sh, int sw, int W, const void* p0, const void* p1,
+               const void* p2) {
+    return R == 3 && S == 3 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && W % 4 == 0 && W > 0 &&
+           ((uintptr_t)p0 | (uintptr_t)p1 | (uintptr_t)p2) % 16 == 0;
+}
+
 bool pair_path(int R, int S, int ph, int pw, int sh, int sw, int W, const void* p0, const void* p1) {
     return R == 2 && S == 2 && sh == 2 && sw == 2 && ph == 0 && pw == 0 && W % 2 == 0 &&
            ((uintptr_t)p0 | (uintptr_t)p1) % 8 == 0;
@@ -387,7 +485,10 @@ int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int 
         // Clear with a kernel (all-zero bits are int 0), not a memset node,
         // so that the call can be captured into a graph.
         SEERA_TRY(fill_f32(reinterpret_cast<float*>(mask), 0.f, (size_t)nin, st));
-        if (R == 2 && S == 2)
+        if (s2p1_path(R, S, ph, pw, sh, sw, W, x, mask, out))
+            hipLaunchKernelGGL(maxpool_fwd_3x3s2p1, dim3(blocks(nout / 2)), dim3(256), 0, st, x,
+                               out, mask, g, nout / 2);
+        else if (R == 2 && S == 2)
             hipLaunchKernelGGL((maxpool_fwd_general_t<2, 2>), dim3(blocks(nout)), dim3(256), 0,
                                st, x, out, mask, g, nout);
         else if (R == 3 && S == 3)
@@ -412,6 +513,9 @@ int maxpool_bwd(const float* dout, const int* mask, float* dx, int B, int C, int
     else if (sh >= R && sw >= S)
         hipLaunchKernelGGL(maxpool_bwd_cells, dim3(blocks(nout)), dim3(256), 0, st, dout, mask,
                            dx, g, nout);
+    else if (s2p1_path(R, S, ph, pw, sh, sw, W, mask, dx, mask))
+        hipLaunchKernelGGL(maxpool_bwd_3x3s2p1, dim3(blocks(nin / 4)), dim3(256), 0, st, dout,
+                           mask, dx, g, nin / 4);
     else
         SEERA_TRY(launch_bwd_general(dout, mask, dx, g, nin, st));
     SEERA_HIP_TRY(hipGetLastError());

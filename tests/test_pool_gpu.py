@@ -167,3 +167,30 @@ def test_unaligned_pointers_match_aligned():
         got_dx = pd.to_array((n + 1,))[1:].reshape(x.shape)
         assert np.array_equal(po.to_array(out.shape), out)
         assert np.array_equal(got_m, mask) and np.array_equal(got_dx, dx)
+
+
+@pytest.mark.parametrize("H,W", [(9, 12), (8, 8), (1, 4), (13, 20)])
+def test_3x3_s2_p1_vector_path_matches_general(H, W):
+    """3x3 stride 2 padding 1 with W % 4 == 0 and 16-byte aligned tensors runs
+    the 16-byte kernels; 4-byte-aligned pointers take the general kernels.
+    Small integers (many ties, padded origins with every element below 0):
+    both give the oracle's bits."""
+    x = np.random.default_rng(H * 31 + W).integers(-3, 2, (2, 3, H, W)).astype(np.float32)
+    out, mask = hip_maxpool(x, 3, 3, 1, 2)
+    ro, rm = pool.maxpool_fwd(x, 3, 3, 1, 1, 2, 2)
+    assert np.array_equal(out, ro) and np.array_equal(mask, rm)
+    dout = np.random.default_rng(H + W).standard_normal(out.shape).astype(np.float32)
+    dx = hip_maxpool_bwd(dout, mask, 3, 3, 1, 2)
+    assert np.array_equal(dx, pool.maxpool_bwd(dout, rm, 3, 3, 1, 1, 2, 2))
+    N, C = x.shape[:2]
+    n = x.size
+    with DeviceBuffer(4 * n + 4) as px, DeviceBuffer(out.nbytes) as po, \
+            DeviceBuffer(4 * n + 4) as pm, DeviceBuffer.from_array(dout) as pg, \
+            DeviceBuffer(4 * n + 4) as pd:
+        capi.check(capi.load().seera_hip_memcpy_h2d(px.ptr + 4, x.ctypes.data, x.nbytes))
+        args = (N, C, H, W, 3, 3, 1, 1, 2, 2)
+        capi.call("seera_hip_maxpool_fwd", px.ptr + 4, po.ptr, pm.ptr + 4, *args)
+        capi.call("seera_hip_maxpool_bwd", pg.ptr, pm.ptr + 4, pd.ptr + 4, *args)
+        assert np.array_equal(po.to_array(out.shape), out)
+        assert np.array_equal(pm.to_array((n + 1,), np.int32)[1:].reshape(x.shape), mask)
+        assert np.array_equal(pd.to_array((n + 1,))[1:].reshape(x.shape), dx)
