@@ -108,6 +108,7 @@ struct GemmProblem {
     int act;               // EPI: kActNone or kActRelu
     float* colsum;         // COLSUM: [splits][N]
     static constexpr bool kEpi = EPI;
+    static constexpr bool kStoreCol = EPI;
     static constexpr bool kColSum = COLSUM;
     static constexpr bool kPipe = true;  // StageKC / StageMNC load without branches
 
@@ -148,6 +149,38 @@ struct GemmProblem {
     __device__ __forceinline__ void init_b(S&, int, int) const {}
     __device__ __forceinline__ void store_colsum(int n, int z, float v) const {
         if (n < N) colsum[(int64_t)z * N + n] = v;
+    }
+    // One accumulator column (rows m[r] of column n) under the epilogue: the
+    // bias of the column is read once, and (ReLU backward) every mask value
+    // before any output is written, so no load waits behind a store it might
+    // alias. The arithmetic is store()'s.
+    __device__ __forceinline__ void store_col(int n, int z, const int (&m)[16],
+                                              const float (&v)[16]) const {
+        if constexpr (EPI) {
+            if (split_stride == 0) {
+                if (act == kActReluGrad) {
+                    float mk[16];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        mk[r] = m[r] < M ? mask[(int64_t)m[r] * ldc + n] : 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (m[r] < M) C[(int64_t)m[r] * ldc + n] = v[r] * mk[r];
+                    return;
+                }
+                const float b = bias ? bias[n] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    if (m[r] >= M) continue;
+                    const int64_t i = (int64_t)m[r] * ldc + n;
+                    epilogue(C + i, mask ? mask + i : nullptr, v[r], b, act);
+                }
+                return;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (m[r] < M) C[z * split_stride + (int64_t)m[r] * ldc + n] = v[r];
     }
     __device__ __forceinline__ void store(int m, int n, int z, float v) const {
         const int64_t i = z * split_stride + (int64_t)m * ldc + n;

@@ -42,6 +42,37 @@ struct has_colsum<P, std::void_t<decltype(P::kColSum)>> : std::bool_constant<P::
 // holder threads (NH of them, each with the sums of columns col0 + q and a
 // reduction slot in 0 .. NH/(ROWS/4) - 1 among the holders of that column
 // group; slot -1: not a holder) put their sums in LDS, then the first ROWS
+// Problems that declare `static constexpr bool kStoreCol = true` take the 16
+// accumulator rows of one output column at once (store_col): a fused
+// epilogue can then read its per-column and per-element inputs before any
+// output is written.
+template <class P, class = void>
+struct has_store_col : std::false_type {};
+template <class P>
+struct has_store_col<P, std::void_t<decltype(P::kStoreCol)>> : std::bool_constant<P::kStoreCol> {};
+
+// Writes accumulator tile column n of a wave: rows mbase + 8*(r/4) + 4*(lane/32)
+// + r%4 of the 32x32 MFMA layout (rows >= M are skipped by the problem).
+template <class P>
+__device__ __forceinline__ void store_acc_col(const P& p, const floatx16& a, int mbase, int n, int z,
+                                              int lane) {
+    if constexpr (has_store_col<P>::value) {
+        int m[16];
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            m[r] = mbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            v[r] = a[r];
+        }
+        p.store_col(n, z, m, v);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < p.M) p.store(m, n, z, a[r]);
+        }
+    }
+}
 // threads add the slots in order.
 template <int ROWS, int NH, class P>
 __device__ __forceinline__ void colsum_finish(const P& p, const float (&cs)[4], int col0, int slot,
@@ -134,12 +165,7 @@ __global__ __launch_bounds__(WM* WN * 64) void igemm_kernel(const P p) {
         const int n = n0 + wn0 + j * 32 + (lane & 31);
         if (n >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.M) p.store(m, n, z, acc[i][j][r]);
-            }
+        for (int i = 0; i < TM; ++i) store_acc_col(p, acc[i][j], m0 + wm0 + i * 32, n, z, lane);
     }
 }
 
@@ -322,12 +348,7 @@ __device__ __forceinline__ void pipe_body(const P& p, int bid, int nblk, int z_s
         const int n = n0 + wn0 + j * 32 + (lane & 31);
         if (n >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.M) p.store(m, n, z, acc[i][j][r]);
-            }
+        for (int i = 0; i < TM; ++i) store_acc_col(p, acc[i][j], m0 + wm0 + i * 32, n, z, lane);
     }
 }
 
@@ -413,12 +434,7 @@ __device__ __forceinline__ void ws_consume(const P& p, const half_t* smem, int m
         const int n = n0 + wn0 + j * 32 + (lane & 31);
         if (n >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.M) p.store(m, n, z, acc[i][j][r]);
-            }
+        for (int i = 0; i < TM; ++i) store_acc_col(p, acc[i][j], m0 + wm0 + i * 32, n, z, lane);
     }
 }
 
