@@ -317,14 +317,6 @@ hipError_t launch_nch(const Stride2Args& a, int nblocks, int nftiles, hipStream_
     return hipGetLastError();
 }
 
-int cus_of_device() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 }  // namespace
 
 int stride2_conv(const float* in, const float* Wt, float* out, int B, int C, int H, int W, int F,
@@ -352,7 +344,7 @@ int stride2_conv(const float* in, const float* Wt, float* out, int B, int C, int
     // Strip length: fewest rounds of one block per CU, each costing about
     // (steps + 1.5) step times (the prologue fetches the weights and the first
     // rows unhidden).
-    const int ncu = cus_of_device();
+    const int ncu = device_cus();
     int best_l = kRows;
     double best_cost = 1e30;
     for (int L = kRows; L < a.Ho + kRows; L += kRows) {
