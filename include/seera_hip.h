@@ -46,6 +46,18 @@ int seera_hip_malloc(void **out, size_t nbytes);
  * handed out again; if an *_async entry point (or a memset / device copy) may
  * still have work queued, the device is synchronized first, as cudaFree does. */
 int seera_hip_free(void *ptr);
+/* No counterpart in the reference (its cuda_malloc / cuda_free synchronize):
+ * stream-ordered allocation, for callers that queue work on streams.
+ * seera_hip_malloc_async returns a block that work queued on `stream` after
+ * the call may use. seera_hip_free_async(ptr, stream) returns a block from
+ * either malloc without synchronizing: work queued on `stream` before the
+ * free may still use it; a later seera_hip_malloc_async on the same stream
+ * may get it back at once (stream order), any other request only once that
+ * work has completed (an event recorded at the free). Both fail with
+ * SEERA_ERR_INVALID_ARGUMENT while `stream` is being captured into a graph;
+ * free_async fails for pointers this allocator did not hand out. */
+int seera_hip_malloc_async(void **out, size_t nbytes, void *stream);
+int seera_hip_free_async(void *ptr, void *stream);
 /* No counterpart in the reference: hands every cached block back to HIP
  * (after a device synchronize), for callers that need the memory elsewhere. */
 int seera_hip_empty_cache(void);

@@ -31,6 +31,8 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_device_count": ([], _i),
     "seera_hip_malloc": ([ctypes.POINTER(_vp), _sz], _i),
     "seera_hip_free": ([_vp], _i),
+    "seera_hip_malloc_async": ([ctypes.POINTER(_vp), _sz, _vp], _i),
+    "seera_hip_free_async": ([_vp, _vp], _i),
     "seera_hip_empty_cache": ([], _i),
     "seera_hip_memory_stats": ([ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
     "seera_hip_fill_f32": ([_vp, ctypes.c_float, _sz], _i),

@@ -283,6 +283,17 @@ int seera_hip_free(void* ptr) {
     return guarded([&] { return device_free(ptr); });
 }
 
+int seera_hip_malloc_async(void** out, size_t nbytes, void* stream) {
+    return guarded([&] {
+        if (!out) return fail(SEERA_ERR_INVALID_ARGUMENT, "null out pointer");
+        return device_malloc_async(out, nbytes, as_stream(stream));
+    });
+}
+
+int seera_hip_free_async(void* ptr, void* stream) {
+    return guarded([&] { return device_free_async(ptr, as_stream(stream)); });
+}
+
 int seera_hip_empty_cache(void) {
     return guarded([&] { return device_empty_cache(); });
 }

@@ -109,8 +109,11 @@ int workspace(size_t bytes, void** out, hipStream_t st) {
     return e;
 }
 
+void streams_gone_for_pending(hipStream_t st);
+
 int stream_destroyed(hipStream_t st) {
     if (!st) return SEERA_OK;
+    streams_gone_for_pending(st);
     int dev = 0;
     SEERA_HIP_TRY(hipStreamGetDevice(st, &dev));
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -157,10 +160,22 @@ struct LiveBlock {
     int dev;
     size_t bytes;  // size class
 };
+// A block handed back by device_free_async: free for work queued on `stream`
+// after the free, for anything else once `ev` (recorded on the stream at the
+// free) has completed. stream_gone: the stream was destroyed (its handle may
+// come back for a new stream), so only the event counts.
+struct PendingBlock {
+    void* ptr;
+    hipStream_t stream;
+    hipEvent_t ev;
+    bool stream_gone;
+};
 std::mutex g_alloc_mu;
 std::unordered_map<void*, LiveBlock> g_live;
 std::map<std::pair<int, size_t>, std::vector<void*>> g_cached;
-size_t g_live_bytes = 0, g_cached_bytes = 0;
+std::map<std::pair<int, size_t>, std::vector<PendingBlock>> g_pending;
+std::map<int, std::vector<hipEvent_t>> g_spare_events;  // per device, recorded events to reuse
+size_t g_live_bytes = 0, g_cached_bytes = 0, g_pending_bytes = 0;
 std::atomic<bool> g_async_pending{false};
 
 size_t size_class(size_t n) {
@@ -202,27 +217,91 @@ int release_cached(int dev) {
     }
     return SEERA_OK;
 }
-}  // namespace
+// Takes a block of (dev, cls) from the pending list that work on `st` may use
+// now: one freed on `st` itself (stream order puts this request after that
+// free), else one whose free event has completed. Caller holds g_alloc_mu.
+void* take_pending(int dev, size_t cls, hipStream_t st, bool same_stream_ok) {
+    auto it = g_pending.find({dev, cls});
+    if (it == g_pending.end()) return nullptr;
+    std::vector<PendingBlock>& v = it->second;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (size_t i = v.size(); i-- > 0;) {
+            const PendingBlock& b = v[i];
+            bool ok;
+            if (pass == 0) {
+                ok = same_stream_ok && !b.stream_gone && b.stream == st;
+            } else {
+                const hipError_t q = hipEventQuery(b.ev);
+                if (q != hipSuccess && q != hipErrorNotReady) (void)hipGetLastError();
+                ok = q == hipSuccess;
+            }
+            if (!ok) continue;
+            void* p = b.ptr;
+            g_spare_events[dev].push_back(b.ev);
+            v.erase(v.begin() + (ptrdiff_t)i);
+            g_pending_bytes -= cls;
+            return p;
+        }
+    }
+    return nullptr;
+}
 
-void note_async_work() { g_async_pending.store(true, std::memory_order_release); }
-void note_device_synchronized() { g_async_pending.store(false, std::memory_order_release); }
+// Moves every pending block into the cache (the caller has synchronized the
+// device, so all their events have completed) and destroys the spare events.
+// Caller holds g_alloc_mu.
+void drain_pending(int dev) {
+    for (auto it = g_pending.begin(); it != g_pending.end();) {
+        if (dev >= 0 && it->first.first != dev) {
+            ++it;
+            continue;
+        }
+        for (const PendingBlock& b : it->second) {
+            g_cached[it->first].push_back(b.ptr);
+            g_cached_bytes += it->first.second;
+            g_pending_bytes -= it->first.second;
+            (void)hipEventDestroy(b.ev);
+        }
+        it = g_pending.erase(it);
+    }
+    for (auto it = g_spare_events.begin(); it != g_spare_events.end();) {
+        if (dev >= 0 && it->first != dev) {
+            ++it;
+            continue;
+        }
+        for (hipEvent_t e : it->second) (void)hipEventDestroy(e);
+        it = g_spare_events.erase(it);
+    }
+}
 
-int device_malloc(void** out, size_t nbytes) {
-    *out = nullptr;
-    int dev = 0;
-    SEERA_HIP_TRY(hipGetDevice(&dev));
-    const size_t cls = size_class(nbytes);
-    std::lock_guard<std::mutex> lock(g_alloc_mu);
-    auto it = g_cached.find({dev, cls});
-    if (it != g_cached.end() && !it->second.empty()) {
-        *out = it->second.back();
-        it->second.pop_back();
-        g_cached_bytes -= cls;
-    } else {
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cap != hipStreamCaptureStatusNone;
+}
+
+// The allocation itself: a cached block of the class, a pending one that `st`
+// may use (st == nullptr and same_stream_ok false: only completed ones), or
+// hipMalloc (after a failure: synchronize, reclaim every cached and pending
+// block of the device and retry once). Caller holds g_alloc_mu.
+int alloc_locked(int dev, size_t cls, hipStream_t st, bool same_stream_ok, void** out) {
+    *out = take_pending(dev, cls, st, same_stream_ok);
+    if (!*out) {
+        auto it = g_cached.find({dev, cls});
+        if (it != g_cached.end() && !it->second.empty()) {
+            *out = it->second.back();
+            it->second.pop_back();
+            g_cached_bytes -= cls;
+        }
+    }
+    if (!*out) {
         hipError_t e = hipMalloc(out, cls);
         if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
             (void)hipGetLastError();  // clear the sticky allocation error
             SEERA_HIP_TRY(hipDeviceSynchronize());
+            drain_pending(dev);
             SEERA_TRY(release_cached(dev));
             e = hipMalloc(out, cls);
         }
@@ -234,6 +313,67 @@ int device_malloc(void** out, size_t nbytes) {
     g_live[*out] = LiveBlock{dev, cls};
     g_live_bytes += cls;
     return SEERA_OK;
+}
+}  // namespace
+
+void note_async_work() { g_async_pending.store(true, std::memory_order_release); }
+void note_device_synchronized() { g_async_pending.store(false, std::memory_order_release); }
+
+int device_malloc(void** out, size_t nbytes) {
+    *out = nullptr;
+    int dev = 0;
+    SEERA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    return alloc_locked(dev, size_class(nbytes), nullptr, false, out);
+}
+
+int device_malloc_async(void** out, size_t nbytes, hipStream_t st) {
+    *out = nullptr;
+    if (capturing(st))
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "stream-ordered allocation is not supported during graph capture");
+    int dev = 0;
+    SEERA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    return alloc_locked(dev, size_class(nbytes), st, true, out);
+}
+
+int device_free_async(void* ptr, hipStream_t st) {
+    if (!ptr) return SEERA_OK;
+    if (capturing(st))
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "stream-ordered free is not supported during graph capture");
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    auto it = g_live.find(ptr);
+    if (it == g_live.end())
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "seera_hip_free_async: %p was not allocated by seera_hip_malloc(_async)", ptr);
+    const LiveBlock b = it->second;
+    std::vector<hipEvent_t>& spare = g_spare_events[b.dev];
+    hipEvent_t ev = nullptr;
+    if (!spare.empty()) {
+        ev = spare.back();
+        spare.pop_back();
+    } else {
+        SEERA_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    }
+    const hipError_t e = hipEventRecord(ev, st);
+    if (e != hipSuccess) {
+        spare.push_back(ev);
+        return fail_hip(e, "hipEventRecord for a stream-ordered free");
+    }
+    g_live.erase(it);
+    g_live_bytes -= b.bytes;
+    g_pending[{b.dev, b.bytes}].push_back(PendingBlock{ptr, st, ev, false});
+    g_pending_bytes += b.bytes;
+    return SEERA_OK;
+}
+
+void streams_gone_for_pending(hipStream_t st) {
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    for (auto& kv : g_pending)
+        for (PendingBlock& b : kv.second)
+            if (b.stream == st) b.stream_gone = true;
 }
 
 int device_free(void* ptr) {
@@ -263,13 +403,14 @@ int device_free(void* ptr) {
 int device_empty_cache() {
     std::lock_guard<std::mutex> lock(g_alloc_mu);
     SEERA_HIP_TRY(hipDeviceSynchronize());
+    drain_pending(-1);
     return release_cached(-1);
 }
 
 void device_memory_stats(size_t* live_bytes, size_t* cached_bytes) {
     std::lock_guard<std::mutex> lock(g_alloc_mu);
     if (live_bytes) *live_bytes = g_live_bytes;
-    if (cached_bytes) *cached_bytes = g_cached_bytes;
+    if (cached_bytes) *cached_bytes = g_cached_bytes + g_pending_bytes;
 }
 
 int device_cus() {

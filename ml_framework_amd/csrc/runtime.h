@@ -65,6 +65,11 @@ void workspace_stats(size_t* held, size_t* retired_count);
 // when an *_async entry point may have left work queued.
 int device_malloc(void** out, size_t nbytes);
 int device_free(void* ptr);
+// Stream-ordered: the block is usable by work queued on `st` after the call;
+// a block freed with device_free_async goes to work on its own stream at once
+// and elsewhere once the work queued before the free has completed.
+int device_malloc_async(void** out, size_t nbytes, hipStream_t st);
+int device_free_async(void* ptr, hipStream_t st);
 int device_empty_cache();
 void device_memory_stats(size_t* live_bytes, size_t* cached_bytes);
 // Called by the *_async entry points after they enqueue work, and after every

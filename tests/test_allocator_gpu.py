@@ -111,3 +111,100 @@ def test_free_after_async_work_waits_for_it():
         C.close()
     finally:
         check(lib.seera_hip_stream_destroy(st.value))
+
+
+def _malloc_async(n, st):
+    p = ctypes.c_void_p()
+    check(load().seera_hip_malloc_async(ctypes.byref(p), n, st))
+    return p.value
+
+
+def _matmul_into(c_ptr, a, b, st):
+    """C = A.B queued on st (A, B uploaded to fresh buffers kept alive by the caller)."""
+    A, B = DeviceBuffer.from_array(a), DeviceBuffer.from_array(b)
+    check(load().seera_hip_matmul_async(A.ptr, B.ptr, c_ptr, a.shape[0], b.shape[1], a.shape[1], 1, st))
+    return A, B
+
+
+def test_stream_ordered_reuse_on_one_stream():
+    """seera_hip_free_async then seera_hip_malloc_async on the same stream hands
+    the block back at once, and work queued after it sees its own results."""
+    lib = load()
+    r = np.random.default_rng(3)
+    n = 512
+    a1, b1, a2, b2 = (r.uniform(-1, 1, (n, n)).astype(np.float32) for _ in range(4))
+    st = ctypes.c_void_p()
+    check(lib.seera_hip_stream_create(ctypes.byref(st)))
+    try:
+        p = _malloc_async(n * n * 4, st.value)
+        keep1 = _matmul_into(p, a1, b1, st.value)
+        check(lib.seera_hip_free_async(p, st.value))
+        q = _malloc_async(n * n * 4, st.value)
+        assert q == p
+        keep2 = _matmul_into(q, a2, b2, st.value)
+        check(lib.seera_hip_stream_synchronize(st.value))
+        got = np.empty((n, n), np.float32)
+        check(lib.seera_hip_memcpy_d2h(got.ctypes.data, q, got.nbytes))
+        assert_parity(got, fp16r(a2).astype(np.float64) @ fp16r(b2), "C after reuse")
+        check(lib.seera_hip_free_async(q, st.value))
+        del keep1, keep2
+    finally:
+        check(lib.seera_hip_stream_destroy(st.value))
+
+
+def test_stream_ordered_free_waits_for_other_streams():
+    """A block freed on one stream with work still queued there is not handed
+    to another stream until that work has completed; afterwards it is."""
+    lib = load()
+    n = 4096
+    r = np.random.default_rng(5)
+    a = r.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = r.uniform(-1, 1, (n, n)).astype(np.float32)
+    s1, s2 = ctypes.c_void_p(), ctypes.c_void_p()
+    check(lib.seera_hip_stream_create(ctypes.byref(s1)))
+    check(lib.seera_hip_stream_create(ctypes.byref(s2)))
+    try:
+        A, B = DeviceBuffer.from_array(a), DeviceBuffer.from_array(b)
+        p = _malloc_async(n * n * 4, s1.value)
+        e0, e1 = Event(), Event()
+        e0.record(s1.value)
+        for _ in range(8):  # ~1 ms of work writing p
+            check(lib.seera_hip_matmul_async(A.ptr, B.ptr, p, n, n, n, 1, s1.value))
+        check(lib.seera_hip_free_async(p, s1.value))
+        e1.record(s1.value)
+        q = _malloc_async(n * n * 4, s2.value)
+        try:
+            e0.elapsed_ms(e1)
+            s1_done = True
+        except capi.SeeraError:
+            s1_done = False  # the GEMMs are still running
+        if not s1_done:
+            assert q != p
+        check(lib.seera_hip_free_async(q, s2.value))
+        check(lib.seera_hip_stream_synchronize(s1.value))
+        check(lib.seera_hip_stream_synchronize(s2.value))
+        p2 = _malloc_async(n * n * 4, s2.value)
+        assert p2 in (p, q)  # both frees have completed: either block may come back
+        got = np.empty((n, n), np.float32)
+        check(lib.seera_hip_memcpy_d2h(got.ctypes.data, p, got.nbytes))
+        rows = np.arange(0, n, 511)
+        assert_parity(got[rows], fp16r(a[rows]).astype(np.float64) @ fp16r(b), "C rows")
+        check(lib.seera_hip_free_async(p2, s2.value))
+        A.close()
+        B.close()
+    finally:
+        check(lib.seera_hip_stream_destroy(s1.value))
+        check(lib.seera_hip_stream_destroy(s2.value))
+
+
+def test_free_async_rejects_foreign_pointers_and_counts_pending_bytes():
+    lib = load()
+    check(lib.seera_hip_empty_cache())
+    p = _malloc_async(1 << 20, None)
+    assert lib.seera_hip_free_async(p + 256, None) == capi.SEERA_ERR_INVALID_ARGUMENT
+    live0, cached0 = _stats()
+    check(lib.seera_hip_free_async(p, None))
+    live1, cached1 = _stats()
+    assert live1 == live0 - (1 << 20) and cached1 == cached0 + (1 << 20)
+    check(lib.seera_hip_empty_cache())
+    assert _stats()[1] == 0
