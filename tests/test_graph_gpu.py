@@ -276,3 +276,27 @@ def test_async_calls_on_two_streams(lib):
     finally:
         for s in streams:
             lib.seera_hip_stream_destroy(s)
+
+
+def test_convT_backward_graph(lib, stream):
+    """ConvTranspose2D config 5 backward (weight prep, stride-2 dX, stride-2 dW
+    partials and their reduce) captured and replayed."""
+    r = np.random.default_rng(4)
+    N, Ci, H, W, Co = 32, 128, 28, 28, 64
+    x = DeviceBuffer(N * Ci * H * W * 4)
+    dy = DeviceBuffer(N * Co * 56 * 56 * 4)
+    w = DeviceBuffer.from_array((r.standard_normal((Ci, Co, 4, 4)) * 0.05).astype(np.float32))
+    dx, dw = DeviceBuffer(N * Ci * H * W * 4), DeviceBuffer(Ci * Co * 16 * 4)
+
+    def seq():
+        capi.check(lib.seera_hip_conv2DTranspose_bwd_async(w.ptr, x.ptr, dy.ptr, dx.ptr, dw.ptr, N,
+                                                           Ci, H, W, Co, 4, 4, 2, 2, 1, 1, stream))
+
+    def make_inputs(rep):
+        g = np.random.default_rng(10 + rep)
+        return [g.standard_normal((N, Ci, H, W)).astype(np.float32),
+                g.standard_normal((N, Co, 56, 56)).astype(np.float32)]
+
+    _replays_match_eager(lib, stream, seq, [(x, None), (dy, None)],
+                         [(dx, (N, Ci, H, W), np.float32), (dw, (Ci, Co, 4, 4), np.float32)],
+                         make_inputs)
