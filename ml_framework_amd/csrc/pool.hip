@@ -34,6 +34,8 @@
 //   * general (overlapping windows): the forward clears the mask and marks
 //     argmaxes from one thread per output; the backward gathers, one thread
 //     per input element, over the covering windows.
+//   * 3x3 stride 2 padding 1 (W % 4 == 0, 16-byte aligned): 16-byte
+//     accesses; the forward writes every mask element once, no clear.
 // Indices are 32-bit: the entry points reject tensors above INT_MAX elements.
 #include "kernels.h"
 #include "runtime.h"
@@ -300,51 +302,115 @@ __global__ __launch_bounds__(256) void maxpool_bwd_general_t(const float* __rest
 }
 
 // 3x3 windows, stride 2, padding 1 (the usual pooling after a stem
-// convolution) with W a multiple of 4: output pair (ho, 2p, 2p + 1) covers
-// input columns 4p - 1 .. 4p + 3 of rows 2ho - 1 .. 2ho + 1, read as one
-// 16-byte load and one 4-byte load per row; each output keeps the general
-// kernel's visit order and tie rule, so the results are the same bits.
-// Wo = W / 2 is even, so the pair is whole.
+// convolution) with W a multiple of 4, in one pass that writes every mask
+// element (no clear). A thread owns output pair (ho, 2p, 2p + 1) for the
+// output rows ho of a segment [ha, hb) of kSegRows rows, and the mask of input
+// columns 4p .. 4p + 3 in rows 2ho and 2ho + 1. Column 4p + j is covered by
+// windows wo = 2p + k with j = 2k - 1 + s (s the column in the window), so the
+// thread evaluates windows 2p, 2p + 1 and, for the mask only, 2p + 2 (input
+// columns 4p - 1 .. 4p + 5: one 4-byte, one 16-byte and one 8-byte load per
+// row). Row 2ho is covered by window row ho alone and row 2ho + 1 also by
+// ho + 1, so the thread walks down its segment carrying the previous window
+// row's argmaxes and evaluates window row hb as well when it exists (for the
+// mask of row 2hb - 1, not stored). An element is 1 when it is the argmax of
+// any window, the outcome the clear-and-mark kernels give; each window keeps
+// their visit order and tie rule, so out and mask are the same bits. Wo = W / 2
+// is even, so the pair is whole.
+constexpr int kSegRows = 7;
+
 __global__ __launch_bounds__(256) void maxpool_fwd_3x3s2p1(const float* __restrict__ x,
                                                            float* __restrict__ out,
                                                            int* __restrict__ mask, PoolGeom g,
-                                                           unsigned npairs) {
+                                                           FastDiv dseg, unsigned nthreads) {
     const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= npairs) return;
-    const unsigned t = fdiv(i, g.dWo2), pp = i - t * (unsigned)(g.Wo / 2);
-    const unsigned bc = fdiv(t, g.dHo), ho = t - bc * g.Ho;
+    if (i >= nthreads) return;
+    const unsigned np = (unsigned)(g.W / 4);
+    const unsigned t = fdiv(i, g.dW4), pp = i - t * np;
+    const unsigned bc = fdiv(t, dseg), seg = t - bc * dseg.d;
     const unsigned plane = bc * (unsigned)(g.H * g.W);
     const float* xp = x + plane;
-    const int h0 = 2 * (int)ho - 1, c0 = 4 * (int)pp;
-    float v[3][5];
-    bool okr[3];
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-        const int h = h0 + r;
-        okr[r] = h >= 0 && h < g.H;
+    int* mp = mask + plane;
+    float* op = out + bc * (unsigned)(g.Ho * g.Wo) + 2 * pp;
+    const int c0 = 4 * (int)pp;
+    const bool has2 = c0 + 4 < g.W;  // window 2p + 2 exists
+    const int ha = (int)seg * kSegRows, hb = min(ha + kSegRows, g.Ho);
+    // Input row h at columns c0 - 1 .. c0 + 5 (zeros outside the image).
+    auto load_row = [&](int h, float (&v)[7], bool& ok) {
+        ok = h >= 0 && h < g.H;
         const float* row = xp + h * g.W;
-        const float4 q = okr[r] ? *reinterpret_cast<const float4*>(row + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        v[r][0] = okr[r] && c0 > 0 ? row[c0 - 1] : 0.f;
-        v[r][1] = q.x; v[r][2] = q.y; v[r][3] = q.z; v[r][4] = q.w;
+        const float4 q = ok ? *reinterpret_cast<const float4*>(row + c0)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float2 e = ok && has2 ? *reinterpret_cast<const float2*>(row + c0 + 4)
+                                    : make_float2(0.f, 0.f);
+        v[0] = ok && c0 > 0 ? row[c0 - 1] : 0.f;
+        v[1] = q.x; v[2] = q.y; v[3] = q.z; v[4] = q.w;
+        v[5] = e.x; v[6] = e.y;
+    };
+    float rv[3][7];
+    bool okr[3];
+    load_row(2 * ha - 1, rv[0], okr[0]);
+    // Window row ho's argmax (3 r + s, or -1) for windows 2p + k.
+    int prev[3] = {-1, -1, -1};
+    // Mask bits of the thread's 4 columns from window arg a's row r.
+    auto mark = [](const int (&a)[3], int r, int (&m)[4]) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int s = 0; s < 3; ++s) {
+                const int j = 2 * k - 1 + s;
+                if (j >= 0 && j < 4 && a[k] == 3 * r + s) m[j] = 1;
+            }
+    };
+    auto store_mask = [&](int h, const int (&m)[4]) {
+        if (h < g.H)
+            *reinterpret_cast<int4*>(mp + h * g.W + c0) = make_int4(m[0], m[1], m[2], m[3]);
+    };
+    const int hend = hb < g.Ho ? hb : hb - 1;
+    for (int ho = ha; ho <= hend; ++ho) {
+        load_row(2 * ho, rv[1], okr[1]);
+        load_row(2 * ho + 1, rv[2], okr[2]);
+        int cur[3];
+        float best[2];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int w0 = c0 - 1 + 2 * k;  // window's first column
+            float b = okr[0] && w0 >= 0 ? rv[0][2 * k] : 0.f;  // the origin, or 0 in the padding
+            int arg = -1;
+#pragma unroll
+            for (int r = 0; r < 3; ++r)
+#pragma unroll
+                for (int s = 0; s < 3; ++s)
+                    if (okr[r] && w0 + s >= 0 && b <= rv[r][2 * k + s]) {
+                        b = rv[r][2 * k + s];
+                        arg = 3 * r + s;
+                    }
+            if (k < 2) best[k] = b;
+            cur[k] = k < 2 || has2 ? arg : -1;
+        }
+        if (ho < hb) *reinterpret_cast<float2*>(op + ho * g.Wo) = make_float2(best[0], best[1]);
+        if (ho > ha) {
+            // rows 2(ho - 1) (window row ho - 1) and 2ho - 1 (ho - 1 and ho)
+            int m0[4] = {0, 0, 0, 0}, m1[4] = {0, 0, 0, 0};
+            mark(prev, 1, m0);
+            mark(prev, 2, m1);
+            mark(cur, 0, m1);
+            store_mask(2 * ho - 2, m0);
+            store_mask(2 * ho - 1, m1);
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) prev[k] = cur[k];
+#pragma unroll
+        for (int q = 0; q < 7; ++q) rv[0][q] = rv[2][q];
+        okr[0] = okr[2];
     }
-    float best[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int w0 = c0 - 1 + 2 * k;  // window's first column (<= W - 3)
-        float b = okr[0] && w0 >= 0 ? v[0][2 * k] : 0.f;  // the origin, or 0 in the padding
-        int arg = -1;
-#pragma unroll
-        for (int r = 0; r < 3; ++r)
-#pragma unroll
-            for (int s2 = 0; s2 < 3; ++s2)
-                if (okr[r] && w0 + s2 >= 0 && b <= v[r][2 * k + s2]) {
-                    b = v[r][2 * k + s2];
-                    arg = (h0 + r) * g.W + w0 + s2;
-                }
-        best[k] = b;
-        if (arg >= 0) mask[plane + (unsigned)arg] = 1;
+    if (hb == g.Ho) {
+        // the plane's last window row: rows 2(Ho - 1) and 2Ho - 1 (if < H)
+        int m0[4] = {0, 0, 0, 0}, m1[4] = {0, 0, 0, 0};
+        mark(prev, 1, m0);
+        mark(prev, 2, m1);
+        store_mask(2 * g.Ho - 2, m0);
+        store_mask(2 * g.Ho - 1, m1);
     }
-    *reinterpret_cast<float2*>(out + (unsigned)(t * g.Wo) + 2 * pp) = make_float2(best[0], best[1]);
 }
 
 // Its backward: one thread per 4 columns 4q .. 4q + 3 of an input row. Row h
@@ -481,14 +547,16 @@ int maxpool_fwd(const float* x, float* out, int* mask, int B, int C, int H, int 
     } else if (sh >= R && sw >= S) {
         hipLaunchKernelGGL(maxpool_fwd_cells, dim3(blocks(nout)), dim3(256), 0, st, x, out, mask,
                            g, nout);
+    } else if (s2p1_path(R, S, ph, pw, sh, sw, W, x, mask, out)) {
+        const unsigned nseg = (unsigned)((g.Ho + kSegRows - 1) / kSegRows);
+        const unsigned nt = (unsigned)B * C * nseg * (unsigned)(W / 4);
+        hipLaunchKernelGGL(maxpool_fwd_3x3s2p1, dim3(blocks(nt)), dim3(256), 0, st, x, out, mask,
+                           g, make_fastdiv(nseg), nt);
     } else {
         // Clear with a kernel (all-zero bits are int 0), not a memset node,
         // so that the call can be captured into a graph.
         SEERA_TRY(fill_f32(reinterpret_cast<float*>(mask), 0.f, (size_t)nin, st));
-        if (s2p1_path(R, S, ph, pw, sh, sw, W, x, mask, out))
-            hipLaunchKernelGGL(maxpool_fwd_3x3s2p1, dim3(blocks(nout / 2)), dim3(256), 0, st, x,
-                               out, mask, g, nout / 2);
-        else if (R == 2 && S == 2)
+        if (R == 2 && S == 2)
             hipLaunchKernelGGL((maxpool_fwd_general_t<2, 2>), dim3(blocks(nout)), dim3(256), 0,
                                st, x, out, mask, g, nout);
         else if (R == 3 && S == 3)

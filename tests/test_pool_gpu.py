@@ -32,7 +32,7 @@ def hip_maxpool(x, KH, KW, p, s):
     Ho, Wo = pool.out_extent(H, p, KH, s), pool.out_extent(W, p, KW, s)
     with DeviceBuffer.from_array(x) as px, DeviceBuffer(max(N * C * Ho * Wo, 1) * 4) as po, \
             DeviceBuffer(x.nbytes) as pm:
-        pm.fill(0x7F)  # the entry point clears the mask itself
+        pm.fill(0x7F)  # every mask element is written
         capi.call("seera_hip_maxpool_fwd", px.ptr, po.ptr, pm.ptr, N, C, H, W, KH, KW, p, p, s, s)
         return po.to_array((N, C, Ho, Wo)), pm.to_array(x.shape, np.int32)
 
@@ -169,10 +169,11 @@ def test_unaligned_pointers_match_aligned():
         assert np.array_equal(got_m, mask) and np.array_equal(got_dx, dx)
 
 
-@pytest.mark.parametrize("H,W", [(9, 12), (8, 8), (1, 4), (13, 20)])
+@pytest.mark.parametrize("H,W", [(9, 12), (8, 8), (1, 4), (13, 20), (31, 8), (40, 12)])
 def test_3x3_s2_p1_vector_path_matches_general(H, W):
     """3x3 stride 2 padding 1 with W % 4 == 0 and 16-byte aligned tensors runs
-    the 16-byte kernels; 4-byte-aligned pointers take the general kernels.
+    the 16-byte kernels (the forward in segments of 7 output rows: H = 31 and
+    40 give 3 segments); 4-byte-aligned pointers take the general kernels.
     Small integers (many ties, padded origins with every element below 0):
     both give the oracle's bits."""
     x = np.random.default_rng(H * 31 + W).integers(-3, 2, (2, 3, H, W)).astype(np.float32)
