@@ -83,7 +83,11 @@ struct StreamArgs {
 };
 
 // UC: every phase has 3 column taps (0: any).
-template <int PXG, int UC>
+// Epilogue kinds (template argument of the kernel): none, + bias, + bias
+// then ReLU (the mask, when asked for, with the last).
+constexpr int kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2;
+
+template <int PXG, int UC, int EPI>
 __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int bx = blockIdx.x;
@@ -207,8 +211,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         // Fused epilogue (the bias and ReLU of a Conv2D layer): bias of each of
         // this lane's 4 filters, and the mask image (written when ReLU asks
         // for it, at the output's offsets: mask = out > 0, which is v > 0).
-        const bool epi_on = a.epi.bias || a.epi.act;
-        const bool mask_on = a.epi.mask && a.epi.act == kActRelu;
+        const bool mask_on = EPI == kEpiBiasRelu && a.epi.mask;
         float bv[4];
 #pragma unroll
         for (int fg = 0; fg < 4; ++fg)
@@ -216,11 +219,11 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         const rsrc_t mask_img =
             make_rsrc(mask_on ? a.epi.mask + (int64_t)b * a.F * a.Hout * a.Wout : a.out);
         auto finish = [&](floatx4_t v, int fg) {
-            if (epi_on) {
+            if constexpr (EPI != kEpiNone) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float t = v[j] + bv[fg];
-                    v[j] = a.epi.act == kActRelu ? (t > 0.f ? t : 0.f) : t;
+                    v[j] = EPI == kEpiBiasRelu ? (t > 0.f ? t : 0.f) : t;
                 }
             }
             return v;
@@ -492,15 +495,24 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
 #undef SEERA_STREAM_STORE
 }
 
-template <int PXG, int UC>
-hipError_t launch_pxg(const StreamArgs& a, int nftiles, hipStream_t st) {
-    auto kern = stream_conv_kernel<PXG, UC>;
+template <int PXG, int UC, int EPI>
+hipError_t launch_epi(const StreamArgs& a, int nftiles, hipStream_t st) {
+    auto kern = stream_conv_kernel<PXG, UC, EPI>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)a.lds_bytes);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(a.nblocks, nftiles), dim3(kNT), (size_t)a.lds_bytes, st, a);
     return hipGetLastError();
+}
+
+// The epilogue as a compile-time choice: its arithmetic then sits between the
+// last MFMAs of a step and the barrier with no selects or branches.
+template <int PXG, int UC>
+hipError_t launch_pxg(const StreamArgs& a, int nftiles, hipStream_t st) {
+    if (a.epi.act == kActRelu) return launch_epi<PXG, UC, kEpiBiasRelu>(a, nftiles, st);
+    if (a.epi.bias) return launch_epi<PXG, UC, kEpiBias>(a, nftiles, st);
+    return launch_epi<PXG, UC, kEpiNone>(a, nftiles, st);
 }
 
 }  // namespace
