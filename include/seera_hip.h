@@ -445,6 +445,18 @@ int seera_hip_event_destroy(void *event);
 int seera_hip_stream_create(void **stream);
 int seera_hip_stream_destroy(void *stream);
 int seera_hip_stream_synchronize(void *stream);
+/* Give back the library workspace of a stream the caller created itself
+ * (a framework's stream passed to the _async entry points, not one made by
+ * seera_hip_stream_create): the workspace is freed once the stream's queued
+ * work is done, or kept while a graph is live on the device (freed with the
+ * device's last graph). Call it before destroying such a stream: HIP may hand
+ * the same handle to a new stream, which would otherwise inherit the old
+ * buffer; until then the workspace is held to the end of the process. A
+ * later call on the stream simply starts a new workspace. Streams made by
+ * seera_hip_stream_create release theirs in seera_hip_stream_destroy; the
+ * null stream's workspace is kept (no-op). No counterpart in the reference,
+ * which has no streams. */
+int seera_hip_stream_release_workspace(void *stream);
 
 /* HIP graphs of the _async entry points (no counterpart in the reference,
  * which launches every kernel from Python and synchronizes after each). Begin
@@ -466,7 +478,9 @@ int seera_hip_stream_synchronize(void *stream);
  *     ordered; a replay on another stream must not overlap eager calls on the
  *     capture stream (they share that stream's workspace);
  *   - seera_hip_stream_destroy frees the stream's workspace (or keeps it
- *     while a graph is live on the device).
+ *     while a graph is live on the device); a stream the caller created
+ *     itself gives its workspace back with seera_hip_stream_release_workspace
+ *     before the caller destroys it.
  * The _async entry points clear memory with kernels, not memset nodes. */
 int seera_hip_graph_capture_begin(void *stream);
 int seera_hip_graph_capture_end(void *stream, void **graph_exec);

@@ -82,6 +82,7 @@ PROTOTYPES: dict[str, tuple[list, object]] = {
     "seera_hip_event_destroy": ([_vp], _i),
     "seera_hip_stream_create": ([ctypes.POINTER(_vp)], _i),
     "seera_hip_stream_destroy": ([_vp], _i),
+    "seera_hip_stream_release_workspace": ([_vp], _i),
     "seera_hip_stream_synchronize": ([_vp], _i),
     "seera_hip_graph_capture_begin": ([_vp], _i),
     "seera_hip_graph_capture_end": ([_vp, ctypes.POINTER(_vp)], _i),

@@ -648,6 +648,12 @@ int seera_hip_stream_destroy(void* stream) {
         return (int)SEERA_OK;
     });
 }
+int seera_hip_stream_release_workspace(void* stream) {
+    return guarded([&] {
+        SEERA_TRY(stream_destroyed(as_stream(stream)));  // null stream: kept
+        return (int)SEERA_OK;
+    });
+}
 int seera_hip_graph_capture_begin(void* stream) {
     return guarded([&] {
         if (!stream) return fail(SEERA_ERR_INVALID_ARGUMENT, "capture needs a created stream");

@@ -411,10 +411,16 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         // 4*q4 in image row 0, its ring offset (halves, pixel 4*q4 + pad)
         // within a ring row, its 8-channel group and chunk rotation.
         floatx4 va[kItems][8], vb[kItems][8];  // two steps of items in flight
-        // per item: byte offset poff, and packed: ring offset (bits 0-23),
-        // channel group (24-25), chunk rotation (26-27), row rr (28-29)
-        int poff[kItems], pmeta[kItems];
+        // per item: the byte offset of its 8 channels at step 0's row
+        // (pbase), that row (rbase; past every limit when the thread has no
+        // item), and packed: ring offset (bits 0-23), channel group (24-25),
+        // chunk rotation (26-27), row rr (28-29). Step sn reads row
+        // rbase + 2*sn while that row is below the strip's last dY / X row
+        // and inside the image (rlim, wave-uniform).
+        int pbase[kItems], rbase[kItems], pmeta[kItems];
         constexpr bool pisy[kItems] = {true, false};
+        const int W4 = a.W * 4;
+        const int rlim[kItems] = {min(h0 + Lb + 1, a.H), min(h0 + Lb, a.H)};
 #pragma unroll
         for (int k = 0; k < kItems; ++k) {
             const int it2 = ptid;
@@ -422,20 +428,16 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             const int ir = it2 % row_items;
             const int cg = ir & 3, q4 = (ir >> 2) % a.QW, plane = (ir >> 2) / a.QW;
             const int pad = pisy[k] ? kYPad : kXPad;
-            poff[k] = (((plane * 32 + cg * 8) * a.H) * a.W + 4 * q4) * 4;
+            rbase[k] = rr < 2 ? (pisy[k] ? h0 + 1 : h0) + rr : INT_MAX / 2;
+            pbase[k] = (((plane * 32 + cg * 8) * a.H) * a.W + 4 * q4) * 4 + (rr < 2 ? rbase[k] * W4 : 0);
             pmeta[k] = (plane * (pisy[k] ? PY : PX) + (4 * q4 + pad) * 32) | (cg << 24) |
                        (((2 * q4 + pad / 2) & 3) << 26) | (rr << 28);
         }
         auto load_item = [&](int sn, int k, floatx4 (&v)[8]) {
-            {
-                const int prr = pmeta[k] >> 28;
-                const int row = pisy[k] ? h0 + 1 + 2 * sn + prr : h0 + 2 * sn + prr;
-                const bool ok = prr < 2 && (pisy[k] ? row <= h0 + Lb : row < h0 + Lb) &&
-                                (unsigned)row < (unsigned)a.H;
-                const uint32_t vo = ok ? (uint32_t)(poff[k] + row * a.W * 4) : kBufOOB;
+            const bool ok = rbase[k] + 2 * sn < rlim[k];
+            const uint32_t vo = ok ? (uint32_t)(pbase[k] + 2 * sn * W4) : kBufOOB;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = buf_load4s(pisy[k] ? ysrc : xsrc, vo, j * cstride);
-            }
+            for (int j = 0; j < 8; ++j) v[j] = buf_load4s(pisy[k] ? ysrc : xsrc, vo, j * cstride);
         };
         auto store_item = [&](int sn, int k, const floatx4 (&v)[8]) {
             {
@@ -490,6 +492,9 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
         // item ptid % row_items over its rows (rr = ptid / row_items, + 2
         // per step, and the prologue's rows 1..3).
         __syncthreads();
+        // (the producer index is rebuilt from the wave and lane ids rather
+        // than kept live through the loop, where every register is taken)
+        const int ptid = wave * 64 + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) - kCons;
         floatx4* const red = reinterpret_cast<floatx4*>(smem);
         if (producer && ptid < 2 * row_items) {
             red[2 * ptid] = floatx4{dsum[0], dsum[1], dsum[2], dsum[3]};

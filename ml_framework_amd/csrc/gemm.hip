@@ -150,37 +150,43 @@ struct GemmProblem {
     __device__ __forceinline__ void store_colsum(int n, int z, float v) const {
         if (n < N) colsum[(int64_t)z * N + n] = v;
     }
-    // One accumulator column (rows m[r] of column n) under the epilogue: the
-    // bias of the column is read once, and (ReLU backward) every mask value
-    // before any output is written, so no load waits behind a store it might
-    // alias. The arithmetic is store()'s.
-    __device__ __forceinline__ void store_col(int n, int z, const int (&m)[16],
-                                              const float (&v)[16]) const {
+    // One accumulator column (rows mrow + acc_row(r) of column n) under the
+    // epilogue: the bias of the column is read once, and (ReLU backward)
+    // every mask value before any output is written, so no load waits behind
+    // a store it might alias. The arithmetic is store()'s.
+    __device__ __forceinline__ void store_col(int n, int z, int mrow, const float (&v)[16]) const {
+        const int rem = M - mrow;  // rows acc_row(r) < rem exist
+        const int64_t base = (int64_t)mrow * ldc + n;
         if constexpr (EPI) {
             if (split_stride == 0) {
                 if (act == kActReluGrad) {
+                    const float* const mk0 = mask + base;
+                    float* const c0 = C + base;
                     float mk[16];
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        mk[r] = m[r] < M ? mask[(int64_t)m[r] * ldc + n] : 0.f;
+                        mk[r] = acc_row(r) < rem ? mk0[acc_row(r) * ldc] : 0.f;
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        if (m[r] < M) C[(int64_t)m[r] * ldc + n] = v[r] * mk[r];
+                        if (acc_row(r) < rem) c0[acc_row(r) * ldc] = v[r] * mk[r];
                     return;
                 }
                 const float b = bias ? bias[n] : 0.f;
+                float* const c0 = C + base;
+                float* const m0 = mask ? mask + base : nullptr;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    if (m[r] >= M) continue;
-                    const int64_t i = (int64_t)m[r] * ldc + n;
-                    epilogue(C + i, mask ? mask + i : nullptr, v[r], b, act);
+                    if (acc_row(r) >= rem) continue;
+                    const int64_t i = acc_row(r) * ldc;
+                    epilogue(c0 + i, m0 ? m0 + i : nullptr, v[r], b, act);
                 }
                 return;
             }
         }
+        float* const c0 = C + z * split_stride + base;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-            if (m[r] < M) C[z * split_stride + (int64_t)m[r] * ldc + n] = v[r];
+            if (acc_row(r) < rem) c0[acc_row(r) * ldc] = v[r];
     }
     __device__ __forceinline__ void store(int m, int n, int z, float v) const {
         const int64_t i = z * split_stride + (int64_t)m * ldc + n;

@@ -38,18 +38,20 @@ struct has_colsum : std::false_type {};
 template <class P>
 struct has_colsum<P, std::void_t<decltype(P::kColSum)>> : std::bool_constant<P::kColSum> {};
 
-// End of a kColSum block of row tile 0 (every thread of the block calls it):
-// holder threads (NH of them, each with the sums of columns col0 + q and a
-// reduction slot in 0 .. NH/(ROWS/4) - 1 among the holders of that column
-// group; slot -1: not a holder) put their sums in LDS, then the first ROWS
 // Problems that declare `static constexpr bool kStoreCol = true` take the 16
 // accumulator rows of one output column at once (store_col): a fused
 // epilogue can then read its per-column and per-element inputs before any
-// output is written.
+// output is written. Row r of the column is mrow + kAccRow[r], with mrow the
+// lane's first row: each address is one per-lane base plus a wave-uniform
+// row offset, so no per-row 64-bit offsets stay live beside the accumulators.
 template <class P, class = void>
 struct has_store_col : std::false_type {};
 template <class P>
 struct has_store_col<P, std::void_t<decltype(P::kStoreCol)>> : std::bool_constant<P::kStoreCol> {};
+
+// Row of accumulator element r of a 32x32 MFMA tile, relative to the lane's
+// first row mbase + 4*(lane/32).
+__device__ __forceinline__ constexpr int acc_row(int r) { return 8 * (r >> 2) + (r & 3); }
 
 // Writes accumulator tile column n of a wave: rows mbase + 8*(r/4) + 4*(lane/32)
 // + r%4 of the 32x32 MFMA layout (rows >= M are skipped by the problem).
@@ -57,22 +59,23 @@ template <class P>
 __device__ __forceinline__ void store_acc_col(const P& p, const floatx16& a, int mbase, int n, int z,
                                               int lane) {
     if constexpr (has_store_col<P>::value) {
-        int m[16];
         float v[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            m[r] = mbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            v[r] = a[r];
-        }
-        p.store_col(n, z, m, v);
+        for (int r = 0; r < 16; ++r) v[r] = a[r];
+        p.store_col(n, z, mbase + 4 * (lane >> 5), v);
     } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = mbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int m = mbase + 4 * (lane >> 5) + acc_row(r);
             if (m < p.M) p.store(m, n, z, a[r]);
         }
     }
 }
+
+// End of a kColSum block of row tile 0 (every thread of the block calls it):
+// holder threads (NH of them, each with the sums of columns col0 + q and a
+// reduction slot in 0 .. NH/(ROWS/4) - 1 among the holders of that column
+// group; slot -1: not a holder) put their sums in LDS, then the first ROWS
 // threads add the slots in order.
 template <int ROWS, int NH, class P>
 __device__ __forceinline__ void colsum_finish(const P& p, const float (&cs)[4], int col0, int slot,

@@ -38,7 +38,32 @@ struct HipBackend {
         SEERA_HIP_TRY(e);
         return SEERA_OK;
     }
+    int sync_stream(int dev, const void* stream) {
+        int cur = 0;
+        SEERA_HIP_TRY(hipGetDevice(&cur));
+        if (cur != dev) SEERA_HIP_TRY(hipSetDevice(dev));
+        const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(const_cast<void*>(stream)));
+        if (cur != dev) SEERA_HIP_TRY(hipSetDevice(cur));
+        SEERA_HIP_TRY(e);
+        return SEERA_OK;
+    }
 };
+
+// Whether work queued on `st` now would be captured. A refused query counts
+// as capturing when the refusal itself says a capture is under way
+// (hipErrorStreamCaptureImplicit: the legacy null stream while another stream
+// is capturing in global mode; hipErrorStreamCaptureUnsupported); any other
+// refusal means the stream cannot be captured. The query's sticky error is
+// cleared either way.
+bool stream_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(st, &cap);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return e == hipErrorStreamCaptureImplicit || e == hipErrorStreamCaptureUnsupported;
+    }
+    return cap != hipStreamCaptureStatusNone;
+}
 HipBackend g_hip_backend;
 WorkspacePool<HipBackend> g_pool(g_hip_backend);
 std::mutex g_scratch_mu;
@@ -92,15 +117,9 @@ int workspace(size_t bytes, void** out, hipStream_t st) {
     }
     int dev = 0;
     SEERA_HIP_TRY(hipGetDevice(&dev));
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
-        // Not a capturable stream (the query is refused, e.g. for the legacy
-        // null stream in some runtime states): it is not being captured.
-        (void)hipGetLastError();
-        cap = hipStreamCaptureStatusNone;
-    }
+    const bool cap = stream_capturing(st);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    const int e = g_pool.get(dev, st, bytes, cap != hipStreamCaptureStatusNone, out);
+    const int e = g_pool.get(dev, st, bytes, cap, out);
     if (e == WorkspacePool<HipBackend>::kGrowUnderCapture)
         return fail(SEERA_ERR_INVALID_ARGUMENT,
                     "the workspace must grow to %zu bytes during stream capture: make one eager "
@@ -273,14 +292,7 @@ void drain_pending(int dev) {
     }
 }
 
-bool capturing(hipStream_t st) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    return cap != hipStreamCaptureStatusNone;
-}
+bool capturing(hipStream_t st) { return stream_capturing(st); }
 
 // The allocation itself: a cached block of the class, a pending one that `st`
 // may use (st == nullptr and same_stream_ok false: only completed ones), or

@@ -6,21 +6,24 @@
 //   * one workspace per (device, stream): calls on one stream run in order and
 //     share it, calls on two streams never do;
 //   * a workspace grows on demand (rounded up to 1 MiB) and is kept;
-//   * growing synchronizes the device first (queued kernels may still use the
-//     old buffer); while any executable graph is live on that device the old
-//     buffer is retired instead of freed, since a replay still writes to the
-//     address it was captured with; the device's retired buffers are freed
-//     when its last graph is destroyed;
+//   * growing frees the old buffer after synchronizing its own stream (the
+//     only eager work that can still use it is queued there); while any
+//     executable graph is live on that device the old buffer is retired
+//     instead, with no synchronize at all, since a replay still writes to the
+//     address it was captured with; the device's retired buffers are freed,
+//     after a device synchronize, when its last graph is destroyed;
 //   * growing while the stream is being captured is refused (kGrowUnderCapture):
 //     the capture would record a buffer that a later call could free;
-//   * destroying a stream frees its workspace (retired instead while a graph
-//     is live on the device), so a new stream that gets the same handle
-//     starts empty.
+//   * destroying a stream (or releasing a caller-owned stream's workspace)
+//     frees its workspace after synchronizing that stream (retired instead
+//     while a graph is live on the device), so a new stream that gets the
+//     same handle starts empty.
 //
 // Backend interface (all return 0 on success or a nonzero status):
 //   int alloc(int dev, size_t bytes, void** out);
 //   int release(int dev, void* p);
-//   int sync(int dev);
+//   int sync(int dev);                              whole device
+//   int sync_stream(int dev, const void* stream);   one stream's queued work
 // Not thread-safe by itself; the caller holds a lock.
 #pragma once
 
@@ -48,11 +51,11 @@ public:
         if (bytes > s.bytes) {
             if (capturing) return kGrowUnderCapture;
             if (s.ptr) {
-                if (int e = b_.sync(dev)) return e;
                 if (live_graphs_[dev] > 0) {
                     retired_[dev].push_back(s.ptr);
-                } else if (int e = b_.release(dev, s.ptr)) {
-                    return e;
+                } else {
+                    if (int e = b_.sync_stream(dev, stream)) return e;
+                    if (int e = b_.release(dev, s.ptr)) return e;
                 }
                 s.ptr = nullptr;
                 s.bytes = 0;
@@ -68,8 +71,9 @@ public:
         return 0;
     }
 
-    // The stream is being destroyed: its workspace is freed (after a device
-    // synchronize), or retired while a graph on the device may reference it.
+    // The stream is being destroyed (or its owner gives its workspace back):
+    // the workspace is freed after the stream's queued work, or retired while
+    // a graph on the device may reference it.
     int stream_destroyed(int dev, const void* stream) {
         auto it = bufs_.find({dev, stream});
         if (it == bufs_.end()) return 0;
@@ -80,7 +84,7 @@ public:
             retired_[dev].push_back(p);
             return 0;
         }
-        if (int e = b_.sync(dev)) {
+        if (int e = b_.sync_stream(dev, stream)) {
             retired_[dev].push_back(p);  // freed with the device's graphs, or never
             return e;
         }

@@ -6,6 +6,7 @@
 #include <stdlib.h>
 
 #include <set>
+#include <vector>
 
 #include "workspace_pool.h"
 
@@ -23,6 +24,7 @@ int g_failures = 0;
 struct FakeBackend {
     std::set<void*> live;
     int allocs = 0, releases = 0, syncs = 0;
+    std::vector<const void*> stream_syncs;  // streams synchronized one by one
     bool fail_next_alloc = false;
     ~FakeBackend() {
         for (void* p : live) free(p);  // the pool keeps its buffers until exit
@@ -46,6 +48,10 @@ struct FakeBackend {
     }
     int sync(int) {
         ++syncs;
+        return 0;
+    }
+    int sync_stream(int, const void* stream) {
+        stream_syncs.push_back(stream);
         return 0;
     }
 };
@@ -80,7 +86,8 @@ void growth_without_graphs_frees() {
     CHECK(pool.get(0, kS1, 3 * MiB, false, &q) == 0);
     CHECK(q != nullptr);
     CHECK(!b.live.count(p));                   // old buffer released
-    CHECK(b.syncs == 1);                       // after a device synchronize
+    CHECK(b.stream_syncs.size() == 1 && b.stream_syncs[0] == kS1);  // after its stream's work
+    CHECK(b.syncs == 0);                       // no device-wide synchronize
     CHECK(pool.retired_count() == 0);
     CHECK(pool.held_bytes() == 3 * MiB);
 }
@@ -94,6 +101,7 @@ void growth_with_live_graph_retires() {
     pool.graph_created(kG2, 0);
     CHECK(pool.get(0, kS1, 2 * MiB + 1, false, &q) == 0);
     CHECK(b.live.count(p));                    // a replay still writes to p
+    CHECK(b.syncs == 0 && b.stream_syncs.empty());  // retiring waits for nothing
     CHECK(pool.retired_count() == 1);
     CHECK(pool.get(0, kS1, 5 * MiB, false, &r) == 0);
     CHECK(b.live.count(q) && pool.retired_count() == 2);
@@ -150,6 +158,7 @@ void stream_destroy_frees_or_retires() {
     CHECK(pool.get(0, kS1, 3 * MiB, false, &p) == 0);
     CHECK(pool.stream_destroyed(0, kS1) == 0);
     CHECK(!b.live.count(p) && pool.held_bytes() == 0);
+    CHECK(b.syncs == 0 && b.stream_syncs.size() == 1 && b.stream_syncs[0] == kS1);
     CHECK(pool.get(0, kS1, 10, false, &q) == 0);   // a new stream, same handle: fresh
     CHECK(pool.held_bytes() == MiB);
     pool.graph_created(kG1, 0);
@@ -159,6 +168,18 @@ void stream_destroy_frees_or_retires() {
     CHECK(pool.graph_destroyed(kG1) == 0);
     CHECK(!b.live.count(q) && pool.retired_count() == 0);
     CHECK(pool.get(0, kS2, 10, false, &r) == 0 && r != nullptr);
+}
+
+void growth_syncs_only_its_stream() {
+    FakeBackend b;
+    Pool pool(b);
+    void *p1 = nullptr, *p2 = nullptr, *q = nullptr;
+    CHECK(pool.get(0, kS1, 10, false, &p1) == 0);
+    CHECK(pool.get(0, kS2, 10, false, &p2) == 0);
+    CHECK(pool.get(0, kS2, 4 * MiB, false, &q) == 0);    // S2 grows
+    CHECK(b.live.count(p1) && !b.live.count(p2));       // S1's buffer untouched
+    CHECK(b.stream_syncs.size() == 1 && b.stream_syncs[0] == kS2);
+    CHECK(b.syncs == 0);
 }
 
 }  // namespace
@@ -171,6 +192,7 @@ int main() {
     capture_refuses_growth();
     failed_alloc_leaves_clean_state();
     stream_destroy_frees_or_retires();
+    growth_syncs_only_its_stream();
     if (g_failures) {
         fprintf(stderr, "%d check(s) failed\n", g_failures);
         return 1;

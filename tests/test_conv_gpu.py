@@ -126,3 +126,23 @@ def test_outputs_are_overwritten_not_accumulated():
                       2, 3, 8, 8, 4, 3, 3, 1, 1, 1, 1)
         assert np.array_equal(pdx.to_array(x.shape), ref[0])
         assert np.array_equal(pdw.to_array(w.shape), ref[1])
+
+
+def test_subnormal_fp16_operands_conv_identity_bit_exact():
+    """A 1x1 identity convolution, and a 3x3 one with the identity on the
+    centre tap (the config-4 forward and one-pass backward kernels), return
+    fp16r(X) (and dX = fp16r(dY)) bit for bit on inputs full of fp16
+    subnormals: the conv kernels round with subnormals kept, as
+    __float2half does (convolution.cu:59, 68)."""
+    from tests.test_gemm_gpu import _subnormals
+
+    rng = np.random.default_rng(26)
+    for N, C, H, W, k in [(2, 8, 9, 13, 1), (2, 64, 20, 16, 1), (3, 64, 56, 56, 3)]:
+        x = _subnormals(N * C * H * W, rng).reshape(N, C, H, W)
+        w = np.zeros((C, C, k, k), np.float32)
+        w[np.arange(C), np.arange(C), k // 2, k // 2] = 1.0
+        y = hip_conv_fwd(x, w, 1, k // 2)
+        assert np.array_equal(y, fp16r(x)), ("fwd", N, C, H, W, k)
+        dy = _subnormals(N * C * H * W, rng).reshape(N, C, H, W)
+        dx, _ = hip_conv_bwd(dy, x, w, 1, k // 2)
+        assert np.array_equal(dx, fp16r(dy)), ("dX", N, C, H, W, k)

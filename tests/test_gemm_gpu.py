@@ -71,6 +71,55 @@ def test_identity_returns_fp16_rounding_bit_exact():
         assert np.array_equal(got, fp16r(a)), (M, K)
 
 
+def _subnormals(n, rng):
+    """fp16 subnormals and the fp32 values around them, as __float2half
+    rounds them (GEMM.cu:41,52 keep subnormals): exact subnormals k * 2^-24,
+    fp32 values that round into [2^-24, 2^-14), ties between subnormals,
+    values that round to 0 (below 2^-25, and 2^-25 itself: a tie to even),
+    values just below 2^-14 that round up to the smallest normal, and
+    ordinary values, all with random signs."""
+    t = 2.0 ** -24
+    k = rng.integers(1, 1024, n)
+    parts = [
+        k * t,                                                    # exact subnormals
+        np.exp2(rng.uniform(-25, -14, n)),                        # round into the range
+        (k + 0.5) * t,                                            # ties
+        rng.uniform(0, 2.0 ** -25, n),                            # round to 0
+        np.full(n, 2.0 ** -25),                                   # tie to 0
+        2.0 ** -14 - rng.uniform(0, 2.0 ** -26, n),               # round up to 2^-14
+        rng.uniform(-1, 1, n),                                    # ordinary
+    ]
+    v = np.stack(parts, 1).reshape(-1)[:n] * rng.choice([-1.0, 1.0], n)
+    return v.astype(np.float32)
+
+
+def test_subnormal_fp16_operands_kept_bit_exact():
+    """fp16 subnormal operands pass through the in-kernel rounding and the
+    MFMAs unflushed: A @ I == fp16r(A) and I @ B == fp16r(B) bit for bit, on
+    shapes that take the 64x64, 128x128 and 256x256 tile kernels."""
+    rng = np.random.default_rng(24)
+    for M, K in [(37, 70), (256, 256), (2048, 2048), (4096, 4096)]:
+        a = _subnormals(M * K, rng).reshape(M, K)
+        assert np.count_nonzero(np.abs(fp16r(a)) < 2.0 ** -14) > M * K // 4
+        eye = np.eye(K, dtype=np.float32)
+        got = hip_matmul(a, eye)
+        assert np.array_equal(got, fp16r(a)), ("A@I", M, K)
+        got = hip_matmul(np.eye(M, dtype=np.float32), a)
+        assert np.array_equal(got, fp16r(a)), ("I@B", M, K)
+
+
+def test_subnormal_fp16_operands_backward_bit_exact():
+    """The transposed-operand stagers of the backward keep subnormals too:
+    with A = B = I, dA = dC @ I^T and dB = I^T @ dC both equal fp16r(dC)."""
+    rng = np.random.default_rng(25)
+    for n in (70, 256, 2048):
+        dc = _subnormals(n * n, rng).reshape(n, n)
+        eye = np.eye(n, dtype=np.float32)
+        da, db = hip_matmul_bwd(eye, eye, dc)
+        assert np.array_equal(da, fp16r(dc)), ("dA", n)
+        assert np.array_equal(db, fp16r(dc)), ("dB", n)
+
+
 def test_fp16_overflow_saturates_like_float2half():
     a = np.array([[65519.0, 65520.0, -70000.0]], np.float32)
     got = hip_matmul(a.reshape(3, 1, 1), np.ones((1, 1), np.float32)).reshape(-1)

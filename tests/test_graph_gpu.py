@@ -196,6 +196,38 @@ def test_replay_after_workspace_growth(lib, stream):
     assert _stats(lib)[1] == retired0, "retired workspaces not released with the graph"
 
 
+def test_release_workspace_of_a_callers_stream(lib):
+    """seera_hip_stream_release_workspace frees a stream's workspace once its
+    queued work is done (the held bytes drop by what the stream held); a
+    later call on the stream starts a new workspace and still computes the
+    same result; releasing twice, or a stream that never had one, is a no-op."""
+    st = ctypes.c_void_p()
+    capi.check(lib.seera_hip_stream_create(ctypes.byref(st)))
+    r = np.random.default_rng(6)
+    K = 8192
+    a = DeviceBuffer.from_array(r.uniform(-1, 1, (64, K)).astype(np.float32))
+    b = DeviceBuffer.from_array(r.uniform(-1, 1, (K, 64)).astype(np.float32))
+    c = DeviceBuffer(64 * 64 * 4)
+    try:
+        held0, _ = _stats(lib)
+        _splitk_gemm(lib, a, b, c, 64, 64, K, st.value)  # queued: the release must wait for it
+        held1, _ = _stats(lib)
+        assert held1 > held0, "the split-K call took no workspace"
+        capi.check(lib.seera_hip_stream_release_workspace(st.value))
+        assert _stats(lib)[0] == held0
+        want = c.to_array((64, 64))
+        c.fill(0x7F)
+        _splitk_gemm(lib, a, b, c, 64, 64, K, st.value)
+        capi.check(lib.seera_hip_stream_synchronize(st.value))
+        assert np.array_equal(c.to_array((64, 64)), want)
+        capi.check(lib.seera_hip_stream_release_workspace(st.value))
+        capi.check(lib.seera_hip_stream_release_workspace(st.value))
+        assert _stats(lib)[0] == held0
+        capi.check(lib.seera_hip_stream_release_workspace(None))
+    finally:
+        capi.check(lib.seera_hip_stream_destroy(st.value))
+
+
 def test_growth_under_capture_is_a_clean_error(lib):
     """A call that would have to grow its stream's workspace during capture
     fails with SEERA_ERR_INVALID_ARGUMENT instead of recording a buffer a
