@@ -526,6 +526,7 @@ WORKLOADS = {
     "gemm1024": lambda steps, warmup, st: bench_gemm(1024, steps, warmup, st, True),
     "gemm2048": lambda steps, warmup, st: bench_gemm(2048, steps, warmup, st, True),
     "gemm4096": lambda steps, warmup, st: bench_gemm(4096, steps, warmup, st, False),
+    "gemm8192": lambda steps, warmup, st: bench_gemm(8192, steps, warmup, st, False),
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,
     "convT_cfg5": bench_convT,

@@ -445,12 +445,35 @@ __device__ __forceinline__ void mfma_slice(const half_t* As, const half_t* Bs, i
     }
 }
 
+// gm value asking tile_coords for the round-by-round region order below.
+constexpr int kGmRegions = -16;
+
 // Map a linear workgroup id to (tile_m, tile_n) so that the workgroups one XCD
 // receives (the dispatcher deals ids round-robin over the 8 XCDs) form compact
 // GM-row groups that share A and B panels in that XCD's L2.
+//
+// gm == kGmRegions (one block per CU, tiles_m and tiles_n multiples of 16,
+// more tiles than one round of 256 CUs): each round of 256 blocks covers one
+// 16 x 16-tile region, each XCD a 4 x 8-tile block of it (its 32 CUs), and
+// consecutive rounds walk the regions in snake order, so that each round
+// shares its A row panels or its B column panels with the one before. The
+// plain order instead gives every round all tile rows and 8 tile columns:
+// all of A plus 8 column panels per round, which at 8192^3 (fp32 operands,
+// 512 MB) re-reads A from HBM each round once A and B outgrow the MALL.
 __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_n, int gm,
                                             int& tm, int& tn) {
     constexpr int XCD = 8;
+    if (gm == kGmRegions) {
+        const int x = bid % XCD, j = bid / XCD;   // XCD, and order within it
+        const int round = j >> 5, s = j & 31;     // 32 CUs per XCD
+        const int rn = tiles_n >> 4;              // regions per region row
+        const int rr = round / rn;
+        int rc = round - rr * rn;
+        if (rr & 1) rc = rn - 1 - rc;             // snake
+        tm = 16 * rr + 4 * (x & 3) + (s & 3);
+        tn = 16 * rc + 8 * (x >> 2) + (s >> 2);
+        return;
+    }
     int id = bid;
     if (nblocks % XCD == 0) id = (bid % XCD) * (nblocks / XCD) + bid / XCD;
     const int tiles_m = nblocks / tiles_n;

@@ -203,6 +203,11 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
     p.tiles_n = (p.N + tile_bn(pl.tile) - 1) / tile_bn(pl.tile);
     p.k_split = pl.splits > 1 ? pl.k_split : std::max(p.K, 1);
     p.gm = 4;
+    // The 256x256 tile runs one block per CU: past one round of the CUs its
+    // tiles go region by region (tile_coords).
+    if (pl.tile == Tile::L && pl.splits == 1 && p.M % (16 * 256) == 0 && p.N % (16 * 256) == 0 &&
+        tile_count(pl.tile, p.M, p.N) > kNumCUs)
+        p.gm = kGmRegions;
     if (tile_count(pl.tile, p.M, p.N) > kMaxGridX)
         return fail(SEERA_ERR_INVALID_ARGUMENT, "grid too large (%d x %d)", p.M, p.N);
     float* final_c = p.C;
