@@ -25,7 +25,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 LIB_NAME = "libseera_hip.so"
-HIP_SOURCES = ["gemm.hip", "conv.hip", "conv_band.hip", "conv_stream.hip", "conv_phase2.hip", "conv_stride2.hip", "conv_wgrad.hip", "conv_wgrad_s2.hip", "conv_bwd_fused.hip", "memory.hip", "pool.hip", "tensor_ops.hip", "noalloc.hip", "runtime.cpp", "capi.cpp",
+HIP_SOURCES = ["gemm.hip", "conv.hip", "conv_band.hip", "conv_stream.hip", "conv_split.hip", "conv_phase2.hip", "conv_stride2.hip", "conv_wgrad.hip", "conv_wgrad_s2.hip", "conv_bwd_fused.hip", "memory.hip", "pool.hip", "tensor_ops.hip", "noalloc.hip", "runtime.cpp", "capi.cpp",
                "capi_tensor_ops.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",

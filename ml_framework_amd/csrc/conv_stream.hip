@@ -519,6 +519,8 @@ hipError_t launch_pxg(const StreamArgs& a, int nftiles, hipStream_t st) {
 
 int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     *used = false;
+    SEERA_TRY(split_conv(band, st, used));
+    if (*used) return SEERA_OK;
     if (band.ish != 1 || band.isw != 1 || band.nphase < 1) return SEERA_OK;
     StreamArgs a{};
     a.in = band.in; a.wk = band.wk; a.out = band.out; a.epi = band.epi;
