@@ -19,7 +19,14 @@
 //     consecutive phase columns of one filter for each column phase, which
 //     interleave into 8 consecutive output floats: two 16-byte stores.
 //   * 4 producer waves write the 2 input rows of the next step into the ring
-//     (fp16, channel-last) and issue the loads of the step after it.
+//     (fp16, channel-last) and issue the loads of the step after it; they also
+//     store the outputs: the consumer waves write each step's results into an
+//     LDS staging tile, and during the next step but one the producers take
+//     them out (counting themselves out through an LDS counter the consumers
+//     wait on before they overwrite the tile) and store whole runs of four
+//     output rows of a filter plane. Measured on config 5 with the consumers
+//     storing their results themselves: 6.8 us of the 25 us forward were those
+//     stores (the matrix waves stall on store back-pressure).
 // Every input pixel frame at column offset d = u - ipw[c] is read from LDS
 // once per tap row and serves both column phases where their offsets meet.
 // HBM sees each input element once per 32-filter tile (plus halo rows) and
@@ -58,6 +65,18 @@ constexpr int kPreItems = 3;      // input items per producer thread, prologue
 constexpr int kWC = 32;           // phase columns per block
 constexpr int kND = 3;            // column offsets d read per tap row
 constexpr int kTailPad = 1024;
+// Output staging tile: fp32 [4 output rows][32 filters][8 phase-column quads
+// x 2 column phases], 16 slots of 16 bytes per (row, filter): slot 2*pq + c
+// holds phase columns 4pq .. 4pq + 3 of column phase c (an accumulator as the
+// MFMAs leave it), stored at slot (2*pq + c) ^ (f & 15) so that the
+// consumers' writes (8 lanes: 8 filters at one slot) and the producers'
+// reads (a slot pair of one filter) hit distinct 16-byte slots.
+constexpr int kStageBytes = 4 * 32 * 16 * 16;
+constexpr int kStageItems = 4;    // staged slot pairs per producer thread (4 x 32 x 8 / 256)
+static_assert(kStageItems * 256 >= 4 * 32 * 8, "the producers cover the staging tile");
+__device__ __forceinline__ int stage_off(int r, int f, int slot) {
+    return ((r * 32 + f) * 16 + (slot ^ (f & 15))) * 4;
+}
 
 struct Phase2Args {
     const float* in;     // [B, C, H, W] fp32
@@ -75,6 +94,7 @@ struct Phase2Args {
     int BC4;             // ring pixels per plane
     int NR;              // ring rows
     int64_t lds_bytes;
+    int64_t stage_off;   // byte offset of the staging tile (and its counter after it)
 };
 
 // Weight fragments in the order the consumer waves load them: for filter
@@ -115,6 +135,8 @@ __global__ void prep_phase2_weights(const float* __restrict__ W, half_t* __restr
 template <int NCH>
 __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
     extern __shared__ __attribute__((aligned(16))) half_t ring[];
+    float* const stg = reinterpret_cast<float*>(reinterpret_cast<char*>(ring) + a.stage_off);
+    int* const stg_cnt = reinterpret_cast<int*>(stg + kStageBytes / 4);
     int local = blockIdx.x;
     const int cb = local % a.ncb;
     local /= a.ncb;
@@ -162,6 +184,7 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
                         wv[c][ch][t][u] = wsrc[(((c * NCH + ch) * 2 + t) * 2 + u) * 64];
     } else {
         const int ptid = tid - kCons;
+        if (ptid == 0) *stg_cnt = 0;  // read by the consumers only after step 0's barrier
         const int nitems = (g0 + kRows) * row_items;  // <= kPreItems * kProd (host check)
         floatx4 xv[kPreItems][8];
 #pragma unroll
@@ -216,9 +239,6 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
         constexpr int NQ = kRows * NCH * 2;
         const int kc = lane >> 4;
         const int iph = a.iph[ra];
-        const int f = ftile * 32 + fh * 16 + (lane & 15);
-        const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Hout * a.Wout);
-        const int hw = a.Hout * a.Wout;
         int poff[ND][2];
 #pragma unroll
         for (int di = 0; di < ND; ++di)
@@ -263,28 +283,22 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
                                                          wv[c][ch][t][u], acc[r][pg][c]);
             }
 #undef SEERA_P2_READ
-            // Lane: phase columns pc..pc+3 of filter f for both column phases
-            // -> output columns 2*pc .. 2*pc + 7, two 16-byte stores.
+            // Lane: phase columns pc..pc+3 (phase quad 4*pg + kc) of filter f
+            // for each column phase, staged as they are once the producers
+            // have taken step s-1 out of the tile.
+            while (__hip_atomic_load(stg_cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 4 * s)
+                __builtin_amdgcn_s_sleep(1);
+            const int fl = fh * 16 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const int o = s * kRows + r;
-                const int orow = (2 * (oh0 + o) + ra) * a.Wout;
+            for (int r = 0; r < kRows; ++r)
 #pragma unroll
-                for (int pg = 0; pg < 2; ++pg) {
-                    const int pc = ow0 + pg * 16 + 4 * kc;
-                    const bool ok = o < Lb && pc < a.Wp && f < a.F;
-                    const uint32_t off = ok ? (uint32_t)((f * hw + orow + 2 * pc) * 4) : kBufOOB;
-                    const floatx4_t v0 = {acc[r][pg][0][0], acc[r][pg][1][0], acc[r][pg][0][1],
-                                          acc[r][pg][1][1]};
-                    const floatx4_t v1 = {acc[r][pg][0][2], acc[r][pg][1][2], acc[r][pg][0][3],
-                                          acc[r][pg][1][3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, v0), dst_img,
-                                                           off, 0, 0);
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, v1), dst_img,
-                                                           ok ? off + 16u : kBufOOB, 0, 0);
-                }
-            }
+                for (int pg = 0; pg < 2; ++pg)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c)
+                        *reinterpret_cast<floatx4_t*>(stg + stage_off(2 * r + ra, fl, 2 * (4 * pg + kc) + c)) =
+                            acc[r][pg][c];
         }
+        __syncthreads();  // the last step's results are staged
         return;
     }
 
@@ -347,14 +361,53 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
             }                                                                                \
         }                                                                                    \
     }
+    // Staged outputs: item k of this thread is (k * 256 + ptid) = (f * 4 +
+    // row) * npq + pq, phase quads fastest (four consecutive output rows of a
+    // filter plane are contiguous in HBM when the block spans the row): the
+    // two column phases of phase columns 4pq .. 4pq + 3 interleave into output
+    // columns 8pq .. 8pq + 7. Each item is read and stored in turn (8
+    // registers at a time); the producers count themselves out of the tile
+    // after their last read, at the start of a step whose consumers need the
+    // tile only at its end.
+    const int npq = min(2 * kWC, a.Wout - 2 * ow0) >> 3;
+    const int nst_items = 4 * 32 * npq;
+    const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Hout * a.Wout);
+    auto flush = [&](int st) {  // phase rows 2st, 2st + 1: output rows 4st .. 4st + 3
+#pragma unroll
+        for (int k = 0; k < kStageItems; ++k) {
+            const int idx = k * kProd + ptid;
+            const int pq = idx % npq, fr = idx / npq, fl = fr >> 2, orow = fr & 3;
+            const int f = ftile * 32 + fl;
+            if (idx < nst_items) {
+                const float* base = stg + (orow * 32 + fl) * 64;
+                const int s0 = (2 * pq) ^ (fl & 15);  // column phase 0; phase 1 is s0 ^ 1
+                const floatx4_t e = *reinterpret_cast<const floatx4_t*>(base + s0 * 4);
+                const floatx4_t o = *reinterpret_cast<const floatx4_t*>(base + (s0 ^ 1) * 4);
+                const bool ok = f < a.F && kRows * st + (orow >> 1) < Lb;
+                const uint32_t off = ok ? (uint32_t)(((f * a.Hout + 2 * oh0 + 4 * st + orow) * a.Wout +
+                                                      2 * ow0 + 8 * pq) * 4) : kBufOOB;
+                const floatx4_t lo = {e[0], o[0], e[1], o[1]}, hi = {e[2], o[2], e[3], o[3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, lo), dst_img, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, hi), dst_img,
+                                                       ok ? off + 16u : kBufOOB, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every read has returned
+        if (lane == 0) __hip_atomic_fetch_add(stg_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
     __syncthreads();  // releases step 0 (the prologue wrote its rows)
     SEERA_P2_LOAD(v0, 1)
     for (int g = 1; g < nsteps; ++g) {
+        if (g >= 2) flush(g - 2);  // step g-2's results
         // Ring slots of group g held rows that only step g-2 read.
         SEERA_P2_STORE(v0, g)
         SEERA_P2_LOAD(v0, g + 1)
         __syncthreads();  // releases step g
     }
+    if (nsteps >= 2) flush(nsteps - 2);
+    __syncthreads();  // the last step's results are staged
+    flush(nsteps - 1);
+    __builtin_amdgcn_s_waitcnt(0);
 #undef SEERA_P2_LOAD
 #undef SEERA_P2_STORE
 }
@@ -411,7 +464,8 @@ int phase2_conv(const float* in, const float* Wt, float* out, int B, int C, int 
     a.ncb = (a.Wp + kWC - 1) / kWC;
     a.BC4 = (kWC + kND - 1 + 3 + 3) & ~3;
     a.NR = 2 * kRows + a.ne - 1;
-    a.lds_bytes = (int64_t)a.NR * a.nchunks * a.BC4 * 64 + kTailPad;
+    a.stage_off = (int64_t)a.NR * a.nchunks * a.BC4 * 64 + kTailPad;
+    a.lds_bytes = a.stage_off + kStageBytes + 16;
     if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
     const int row_items = a.nchunks * 4 * (a.BC4 / 4);
     if (kRows * row_items > kProd * kItems || (a.ne - 1 + kRows) * row_items > kPreItems * kProd)
