@@ -291,9 +291,32 @@ int gemm_pair(const GemmArgs& g1, Epi e1, const GemmArgs& g2, float* colsum2, hi
         };
         return span(a_kc, 256, g.lda) < kMaxTileSpanBytes && span(b_kc, 256, g.ldb) < kMaxTileSpanBytes;
     };
-    const bool pairable = g1.M > 0 && g1.N > 0 && g1.K > 0 && g2.M > 0 && g2.N > 0 && g2.K > 0 &&
-                          vec(g1, A1_KC, B1_KC) && vec(g2, A2_KC, B2_KC) &&
-                          span_ok(g1, A1_KC, B1_KC) && span_ok(g2, A2_KC, B2_KC);
+    const bool shapes_ok = g1.M > 0 && g1.N > 0 && g1.K > 0 && g2.M > 0 && g2.N > 0 && g2.K > 0 &&
+                           span_ok(g1, A1_KC, B1_KC) && span_ok(g2, A2_KC, B2_KC);
+    const bool pairable = shapes_ok && vec(g1, A1_KC, B1_KC) && vec(g2, A2_KC, B2_KC);
+    if (shapes_ok && !pairable) {
+        // An edge that is not a multiple of 4 (the N = 10 head of an MLP):
+        // both GEMMs on scalar loads in one launch, when both plans are
+        // unsplit 64x64 tiles within one round of the CUs (a launch costs
+        // ~4.5 us at these sizes, more than the scalar loads of a small
+        // GEMM); otherwise each on its own best path below.
+        const Plan pl1 = plan_tiles(g1.M, g1.N, g1.K, true, true, true);
+        const Plan pl2 = plan_tiles(g2.M, g2.N, g2.K, true, true, true);
+        if (pl1.tile == Tile::S && pl2.tile == Tile::S && pl1.splits == 1 && pl2.splits == 1 &&
+            tile_count(Tile::S, g1.M, g1.N) + tile_count(Tile::S, g2.M, g2.N) <= kNumCUs) {
+            GemmProblem<A1_KC, 1, B1_KC, 1, EPI1> p1{};
+            p1.A = g1.A; p1.B = g1.B; p1.C = g1.C;
+            p1.M = g1.M; p1.N = g1.N; p1.K = g1.K;
+            p1.lda = g1.lda; p1.ldb = g1.ldb; p1.ldc = g1.ldc;
+            p1.bias = e1.bias; p1.mask = e1.mask; p1.act = e1.act;
+            GemmProblem<A2_KC, 1, B2_KC, 1, false, CS2> p2{};
+            p2.A = g2.A; p2.B = g2.B; p2.C = g2.C;
+            p2.M = g2.M; p2.N = g2.N; p2.K = g2.K;
+            p2.lda = g2.lda; p2.ldb = g2.ldb; p2.ldc = g2.ldc;
+            p2.colsum = colsum2;
+            return run_plan_pair<true, true>(p1, pl1, p2, pl2, st);
+        }
+    }
     if (pairable) {
         GemmProblem<A1_KC, 4, B1_KC, 4, EPI1> p1{};
         p1.A = g1.A; p1.B = g1.B; p1.C = g1.C;
