@@ -309,12 +309,21 @@ int gemm_pair(const GemmArgs& g1, Epi e1, const GemmArgs& g2, float* colsum2, hi
             p1.M = g1.M; p1.N = g1.N; p1.K = g1.K;
             p1.lda = g1.lda; p1.ldb = g1.ldb; p1.ldc = g1.ldc;
             p1.bias = e1.bias; p1.mask = e1.mask; p1.act = e1.act;
-            GemmProblem<A2_KC, 1, B2_KC, 1, false, CS2> p2{};
-            p2.A = g2.A; p2.B = g2.B; p2.C = g2.C;
-            p2.M = g2.M; p2.N = g2.N; p2.K = g2.K;
-            p2.lda = g2.lda; p2.ldb = g2.ldb; p2.ldc = g2.ldc;
-            p2.colsum = colsum2;
-            return run_plan_pair<true, true>(p1, pl1, p2, pl2, st);
+            const bool va2 = aligned16(g2.A) && g2.lda % 4 == 0 && (A2_KC ? g2.K : g2.M) % 4 == 0;
+            auto fill2 = [&](auto p2) {
+                p2.A = g2.A; p2.B = g2.B; p2.C = g2.C;
+                p2.M = g2.M; p2.N = g2.N; p2.K = g2.K;
+                p2.lda = g2.lda; p2.ldb = g2.ldb; p2.ldc = g2.ldc;
+                p2.colsum = colsum2;
+                return p2;
+            };
+            // The dB GEMM's A (the layer input, transposed) is aligned even
+            // when dC is not: vector loads there take the MLP cfg3 backward
+            // GEMMs from 24.8 to 20.7 us.
+            using P2V = GemmProblem<A2_KC, 4, B2_KC, 1, false, CS2>;
+            using P2S = GemmProblem<A2_KC, 1, B2_KC, 1, false, CS2>;
+            if (va2) return run_plan_pair<true, true>(p1, pl1, fill2(P2V{}), pl2, st);
+            return run_plan_pair<true, true>(p1, pl1, fill2(P2S{}), pl2, st);
         }
     }
     if (pairable) {
