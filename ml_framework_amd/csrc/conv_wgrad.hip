@@ -48,7 +48,8 @@ struct WStreamArgs {
     float* dbpart;       // [ftiles][nsplit][64] bias-gradient partials (nullptr: none)
     int B, C, H, W, F, Ho, Wo, R, S, ph, pw;
     int L, nstrip, nsplit, nctile;
-    int Wp;              // padded row length (pixels, multiple of 32)
+    int ncol;            // column tiles per row (Wo > 64: tiles of Wp = 64 output columns)
+    int Wp;              // padded row length of a column tile (pixels, multiple of 32)
     int rs;              // LDS row stride in halves (Wp + 16: 2 mod 4 16-byte slots)
     int NR;              // X ring rows (2*kG + R - 1)
     int64_t lds_bytes;
@@ -122,7 +123,9 @@ template <int RR, int SS, int DD>
 __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int split = blockIdx.x, ty = blockIdx.y;
-    const int b = split / a.nstrip, strip = split - b * a.nstrip;
+    const int bs = split / a.ncol, ct = split - bs * a.ncol;
+    const int b = bs / a.nstrip, strip = bs - b * a.nstrip;
+    const int wc0 = ct * a.Wp;                   // first output column of the tile
     const int ftile = ty / a.nctile, ctile = ty - ftile * a.nctile;
     const int ohA = strip * a.L;
     const int Lb = min(a.L, a.Ho - ohA);         // output rows of this strip
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         const int j = it % nxo, rest = it / nxo;
         xch[k] = rest % kTile;
         xrow[k] = it < kG * kTile * nxo ? rest / kTile : kG;
-        xcol[k] = 8 * j - a.pw - dd;
+        xcol[k] = wc0 + 8 * j - a.pw - dd;
         xoff[k] = ((xch[k] * a.H + xrow[k]) * a.W + xcol[k]) * 4;
         xqm[k] = 0;
 #pragma unroll
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         const int j = it % ndo, rest = it / ndo;
         dfl[k] = rest % kTile;
         drow[k] = it < kG * kTile * ndo ? rest / kTile : kG;
-        dcol[k] = 8 * j;
+        dcol[k] = wc0 + 8 * j;
         doff[k] = ((dfl[k] * a.Ho + ohA + drow[k]) * a.Wo + dcol[k]) * 4;
         dqm[k] = (dcol[k] < a.Wo ? 1 : 0) | (dcol[k] + 4 < a.Wo ? 2 : 0);
     }
@@ -336,7 +339,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                     }                                                                      \
                 }                                                                          \
                 *reinterpret_cast<half8*>(xr + slot * xplane + xch[k] * a.rs +             \
-                                          xcol[k] + a.pw + dd) = h;                        \
+                                          xcol[k] - wc0 + a.pw + dd) = h;                  \
             }                                                                              \
         }                                                                                  \
         _Pragma("unroll") for (int k = 0; k < kDI; ++k) {                                  \
@@ -351,7 +354,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                     _Pragma("unroll") for (int q = 0; q < 8; ++q) dsum[k] += v8[q];        \
                 }                                                                          \
                 *reinterpret_cast<half8*>(dr + (o % (2 * kG)) * (kTile * a.rs) +           \
-                                          dfl[k] * a.rs + dcol[k]) = pack8(v8);            \
+                                          dfl[k] * a.rs + dcol[k] - wc0) = pack8(v8);      \
             }                                                                              \
         }                                                                                  \
     }
@@ -425,7 +428,10 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     a.dy = Y; a.x = X;
     a.B = B; a.C = C; a.H = H; a.W = W; a.F = F; a.Ho = Ho; a.Wo = Wo;
     a.R = R; a.S = S; a.ph = ph; a.pw = pw;
-    a.Wp = (Wo + 31) & ~31;
+    // Rows wider than 64 output columns run as column tiles of 64 (the
+    // X halo columns loaded by both neighbours; each dY column by one tile).
+    a.Wp = Wo > 64 ? 64 : (Wo + 31) & ~31;
+    a.ncol = (Wo + a.Wp - 1) / a.Wp;
     // Row stride Wp + 16 halves (2 mod 4 slots of 16 bytes): the fragment
     // reads (16 rows x 4 column chunks per wave) measured free of LDS bank
     // conflicts at that stride and 2-way conflicted at Wp + 8.
@@ -448,12 +454,12 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     const int ncu = device_cus();
     double best = 1e30;
     for (int L = kG; L < Ho + kG; L += kG) {
-        const int64_t blocks = (int64_t)B * ((Ho + L - 1) / L) * ntiles;
+        const int64_t blocks = (int64_t)B * ((Ho + L - 1) / L) * a.ncol * ntiles;
         const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + kG - 1) / kG + 2);
         if (cost < best) { best = cost; a.L = L; }
     }
     a.nstrip = (Ho + a.L - 1) / a.L;
-    a.nsplit = B * a.nstrip;
+    a.nsplit = B * a.nstrip * a.ncol;
     // The kernel's producers reuse the rings for the bias-gradient reduction.
     if (with_db && kProd * kDI * 4 > a.lds_bytes) return SEERA_OK;
     const int nftile = (F + kTile - 1) / kTile;

@@ -54,6 +54,11 @@ CONV2D_STREAM = [
     ("s08", 4, 64, 16, 16, 64, 1, 1, 1, 0),    # 1x1: a GEMM over pixels
     ("s09", 2, 16, 8, 64, 16, 1, 3, 1, 1),     # 1x3, one chunk: a single (chunk, row tap) pair, 2 pixel groups
     ("s10", 2, 8, 6, 16, 8, 1, 3, 1, 1),       # 1x3, one chunk, 1 pixel group
+    # rows wider than 64 pixels: the stride-1 dW pass in column tiles of 64
+    ("s11", 2, 64, 10, 112, 64, 3, 3, 1, 1),   # 2 column tiles (64 + 48)
+    ("s12", 1, 16, 9, 200, 24, 3, 3, 1, 1),    # 4 column tiles (64 x 3 + 8), partial filter tile
+    ("s13", 2, 16, 6, 144, 16, 1, 3, 1, 1),    # 1x3: no halo rows, 3 column tiles
+    ("s14", 1, 72, 5, 68, 8, 3, 3, 1, 1),      # 2 column tiles (64 + 4), 2 channel tiles
 ]
 
 # Edge shapes (not from the reference's tests): 1x1 image and kernel, channel

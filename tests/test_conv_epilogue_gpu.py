@@ -135,8 +135,8 @@ def test_fused_conv_against_oracle(case, act):
         assert np.array_equal(mask[clear], (pre[clear] > 0).astype(np.float32))
 
 
-# (name, N, C, H, W, F, K, stride, pad): the first three take the fused
-# (row-streaming) dW + db pass, the others fall back to a separate db pass.
+# (name, N, C, H, W, F, K, stride, pad): band_s2 and gather_w10 fall back to
+# a separate db pass; the others take db from the dW pass's loads of dY.
 BWD_BIAS = [
     ("stream3x3_cfg4_b4", 4, 64, 56, 56, 64, 3, 1, 1),
     ("stream3x3_2tiles", 3, 128, 20, 20, 96, 3, 1, 1),    # two filter and channel tiles
@@ -144,6 +144,7 @@ BWD_BIAS = [
     ("band_s2", 4, 32, 32, 32, 64, 3, 2, 1),
     ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),
     ("fused_odd", 3, 64, 13, 28, 64, 3, 1, 1),            # one-pass dX + dW + db, odd rows
+    ("stream_wide", 2, 32, 9, 136, 40, 3, 1, 1),          # dW + db in 3 column tiles
 ]
 
 
