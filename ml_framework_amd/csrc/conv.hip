@@ -237,6 +237,48 @@ __global__ void relayout_dgrad_weight(const float* __restrict__ W, float* __rest
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// out [rows, Wp] = in [rows, W] with zeros in columns W..Wp-1 (Wp % 4 == 0):
+// a copy whose rows are float4-aligned for the band and row-streaming kernels.
+__global__ __launch_bounds__(256) void widen_rows(const float* __restrict__ in,
+                                                  float* __restrict__ out, int64_t rows, int W,
+                                                  int Wp) {
+    const int nq = Wp >> 2;
+    const int64_t n = rows * nq;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / nq;
+        const int c0 = (int)(i - row * nq) * 4;
+        const float* src = in + row * W;
+        floatx4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = c0 + j < W ? src[c0 + j] : 0.f;
+        *reinterpret_cast<floatx4*>(out + row * Wp + c0) = v;
+    }
+}
+
+// Copies `n` tensors of rows[i] rows x W[i] floats into one staging buffer,
+// each widened to Wp[i] (a multiple of 4) with zero columns; out[i] receives
+// the copy's address.
+int widen_all(int n, const float* const* in, const int64_t* rows, const int* W, const int* Wp,
+              float** out, hipStream_t st) {
+    size_t total = 0;
+    for (int i = 0; i < n; ++i) total += ((size_t)rows[i] * Wp[i] * 4 + 255) & ~(size_t)255;
+    void* ws = nullptr;
+    SEERA_TRY(staging_workspace(std::max<size_t>(total, 256), &ws, st));
+    char* p = static_cast<char*>(ws);
+    for (int i = 0; i < n; ++i) {
+        out[i] = reinterpret_cast<float*>(p);
+        const int64_t quads = rows[i] * (Wp[i] / 4);
+        const int blocks = (int)std::min<int64_t>((quads + 255) / 256, 4096);
+        if (quads > 0)
+            hipLaunchKernelGGL(widen_rows, dim3(blocks), dim3(256), 0, st, in[i], out[i], rows[i],
+                               W[i], Wp[i]);
+        SEERA_HIP_TRY(hipGetLastError());
+        p += ((size_t)rows[i] * Wp[i] * 4 + 255) & ~(size_t)255;
+    }
+    return SEERA_OK;
+}
+
 }  // namespace
 
 namespace {
@@ -252,6 +294,17 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
     bool used = false;
     SEERA_TRY(band_conv_fwd(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi));
     if (used) return SEERA_OK;
+    if (W % 4 != 0 && R * S <= 16) {
+        // Rows that are not float4-aligned: the band path on a copy of X
+        // widened to a multiple of 4 columns (zeros past W, where the
+        // convolution reads its own zero padding), storing Y at its width.
+        const int Wp = (W + 3) & ~3;
+        const int64_t rows = (int64_t)B * C * H;
+        float* Xw = nullptr;
+        SEERA_TRY(widen_all(1, &X, &rows, &W, &Wp, &Xw, st));
+        SEERA_TRY(band_conv_fwd(Xw, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi, Wp));
+        if (used) return SEERA_OK;
+    }
     // Gather path: any width, any tile size.
     FwdGather g{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)npix};
     const Plan pl = plan_tiles(F, (int)npix, (int)K, true, false);
@@ -364,6 +417,18 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     SEERA_TRY(band_conv_dgrad(Yin, Wconv, out, B, F, Hi, Wi, C, H, W, R, S, sh, sw, ph, pw, st,
                               &used));
     if (used) return SEERA_OK;
+    if (Wi % 4 != 0) {
+        // dY rows that are not float4-aligned: the same on a copy widened to
+        // a multiple of 4 columns (the added columns are zeros, as the dY
+        // positions past Wi are in the transposed convolution).
+        const int Wp = (Wi + 3) & ~3;
+        const int64_t rows = (int64_t)B * F * Hi;
+        float* Yw = nullptr;
+        SEERA_TRY(widen_all(1, &Yin, &rows, &Wi, &Wp, &Yw, st));
+        SEERA_TRY(band_conv_dgrad(Yw, Wconv, out, B, F, Hi, Wp, C, H, W, R, S, sh, sw, ph, pw, st,
+                                  &used));
+        if (used) return SEERA_OK;
+    }
     // Gather path: any width, any stride.
     void* ws = nullptr;
     const int64_t wn = (int64_t)F * C * R * S;
@@ -424,6 +489,27 @@ int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int 
     bool used = false, db_done = false;
     SEERA_TRY(band_conv_wgrad(Y, X, dW, db, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used,
                               &db_done));
+    if (!used && (W % 4 != 0 || Wo % 4 != 0)) {
+        // Rows that are not float4-aligned: the band / row-streaming dW on
+        // copies of X and dY widened with zero columns to a width W2 >= W
+        // (a multiple of 4) whose output width Wo2 >= Wo is one too. The
+        // added dY columns are zero, so they add nothing; the X columns
+        // past W are zeros, as the convolution's padding reads.
+        int W2 = (W + 3) & ~3, Wo2 = 0;
+        for (; W2 < W + 4 * sw + 4; W2 += 4) {
+            Wo2 = (W2 + 2 * pw - S) / sw + 1;
+            if (Wo2 % 4 == 0) break;
+        }
+        if (Wo2 % 4 == 0 && Wo2 >= Wo) {
+            const float* src[2] = {X, Y};
+            const int64_t rows[2] = {(int64_t)B * C * H, (int64_t)B * F * Ho};
+            const int w0[2] = {W, Wo}, w1[2] = {W2, Wo2};
+            float* dst[2] = {nullptr, nullptr};
+            SEERA_TRY(widen_all(2, src, rows, w0, w1, dst, st));
+            SEERA_TRY(band_conv_wgrad(dst[1], dst[0], dW, db, B, C, H, W2, F, R, S, sh, sw, ph, pw,
+                                      st, &used, &db_done));
+        }
+    }
     if (!used) {
         // Gather path: any width, any kernel size.
         // Gathers only: the 64x64 tile, split over pixels.

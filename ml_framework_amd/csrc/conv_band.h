@@ -57,10 +57,12 @@ struct BandConvArgs {
 };
 
 // Forward convolution Y = conv(X, W) (W [F, C, R, S]) when the band path
-// applies (input width % 4 == 0, tile fits LDS); *used reports whether it ran.
+// applies (input row pitch % 4 == 0, tile fits LDS); *used reports whether it
+// ran. x_pitch > W_in: X's rows are x_pitch floats long, columns past W_in
+// zero (a copy widened to a float4 multiple); the output is W_in's.
 int band_conv_fwd(const float* X, const float* W, float* Y, int B, int C, int H, int W_in, int F,
                   int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used,
-                  const ConvEpi& epi = {});
+                  const ConvEpi& epi = {}, int x_pitch = 0);
 
 // Transposed convolution out[B, Cc, H, W] of Y [B, Fc, Hi, Wi] with the conv
 // weight W [Fc, Cc, R, S] (stride, pad of the forward conv), by stride phases.

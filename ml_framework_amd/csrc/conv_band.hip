@@ -1047,10 +1047,12 @@ int reduce_wgrad_partials(const float* part, float* dW, int F, int C, int R, int
 
 int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H, int W, int F,
                   int R, int S, int sh, int sw, int ph, int pw, hipStream_t st, bool* used,
-                  const ConvEpi& epi) {
+                  const ConvEpi& epi, int x_pitch) {
     *used = false;
-    if (W % 4 != 0 || !aligned16(X)) return SEERA_OK;
-    if (R == 4 && S == 4 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && !epi.bias && !epi.act) {
+    const int Wx = x_pitch > W ? x_pitch : W;  // row pitch of X (zeros past W)
+    if (Wx % 4 != 0 || !aligned16(X)) return SEERA_OK;
+    if (R == 4 && S == 4 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && !epi.bias && !epi.act &&
+        Wx == W) {
         // Row streaming with column-parity planes (conv_stride2.hip) when it applies.
         bool done = false;
         SEERA_TRY(stride2_conv(X, Wt, Y, B, C, H, W, F, st, &done));
@@ -1063,7 +1065,7 @@ int band_conv_fwd(const float* X, const float* Wt, float* Y, int B, int C, int H
     a.in = X;
     a.out = Y;
     a.epi = epi;
-    a.B = B; a.C = C; a.H = H; a.W = W;
+    a.B = B; a.C = C; a.H = H; a.W = Wx;
     a.F = F;
     a.Hout = (H + 2 * ph - R) / sh + 1;
     a.Wout = (W + 2 * pw - S) / sw + 1;

@@ -66,6 +66,9 @@ bool stream_capturing(hipStream_t st) {
 }
 HipBackend g_hip_backend;
 WorkspacePool<HipBackend> g_pool(g_hip_backend);
+// Second buffer per (device, stream): operands re-laid out for a kernel that
+// takes workspace() itself (staging_workspace).
+WorkspacePool<HipBackend> g_stage_pool(g_hip_backend);
 std::mutex g_scratch_mu;
 
 // A caller-supplied scratch region that workspace() hands out instead of the
@@ -105,6 +108,30 @@ FixedWorkspace::~FixedWorkspace() {
     g_fixed_owner = nullptr;
 }
 
+namespace {
+int pool_get(WorkspacePool<HipBackend>& pool, size_t bytes, void** out, hipStream_t st) {
+    int dev = 0;
+    SEERA_HIP_TRY(hipGetDevice(&dev));
+    const bool cap = stream_capturing(st);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    const int e = pool.get(dev, st, bytes, cap, out);
+    if (e == WorkspacePool<HipBackend>::kGrowUnderCapture)
+        return fail(SEERA_ERR_INVALID_ARGUMENT,
+                    "the workspace must grow to %zu bytes during stream capture: make one eager "
+                    "call of the same sizes on this stream before capturing",
+                    bytes);
+    return e;
+}
+}  // namespace
+
+int staging_workspace(size_t bytes, void** out, hipStream_t st) {
+    *out = nullptr;
+    if (g_fixed_owner)
+        return fail(SEERA_ERR_INVALID_ARGUMENT, "%s: no staging buffer under a fixed workspace",
+                    g_fixed_owner);
+    return pool_get(g_stage_pool, bytes, out, st);
+}
+
 int workspace(size_t bytes, void** out, hipStream_t st) {
     *out = nullptr;
     if (g_fixed_owner) {
@@ -115,17 +142,7 @@ int workspace(size_t bytes, void** out, hipStream_t st) {
         *out = g_fixed_ptr;
         return SEERA_OK;
     }
-    int dev = 0;
-    SEERA_HIP_TRY(hipGetDevice(&dev));
-    const bool cap = stream_capturing(st);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    const int e = g_pool.get(dev, st, bytes, cap, out);
-    if (e == WorkspacePool<HipBackend>::kGrowUnderCapture)
-        return fail(SEERA_ERR_INVALID_ARGUMENT,
-                    "the workspace must grow to %zu bytes during stream capture: make one eager "
-                    "call of the same sizes on this stream before capturing",
-                    bytes);
-    return e;
+    return pool_get(g_pool, bytes, out, st);
 }
 
 void streams_gone_for_pending(hipStream_t st);
@@ -136,7 +153,9 @@ int stream_destroyed(hipStream_t st) {
     int dev = 0;
     SEERA_HIP_TRY(hipStreamGetDevice(st, &dev));
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    return g_pool.stream_destroyed(dev, st);
+    const int e = g_pool.stream_destroyed(dev, st);
+    const int e2 = g_stage_pool.stream_destroyed(dev, st);
+    return e ? e : e2;
 }
 
 int graph_created(void* exec) {
@@ -144,18 +163,21 @@ int graph_created(void* exec) {
     SEERA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     g_pool.graph_created(exec, dev);
+    g_stage_pool.graph_created(exec, dev);
     return SEERA_OK;
 }
 
 int graph_destroyed(void* exec) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    return g_pool.graph_destroyed(exec);
+    const int e = g_pool.graph_destroyed(exec);
+    const int e2 = g_stage_pool.graph_destroyed(exec);
+    return e ? e : e2;
 }
 
 void workspace_stats(size_t* held, size_t* retired_count) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (held) *held = g_pool.held_bytes();
-    if (retired_count) *retired_count = g_pool.retired_count();
+    if (held) *held = g_pool.held_bytes() + g_stage_pool.held_bytes();
+    if (retired_count) *retired_count = g_pool.retired_count() + g_stage_pool.retired_count();
 }
 
 // ---------------------------------------------------------------------------

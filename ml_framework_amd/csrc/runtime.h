@@ -35,6 +35,10 @@ void clear_error();
 // (a replay still writes to it) until the device's last graph is destroyed.
 // Growing while `st` is being captured fails with SEERA_ERR_INVALID_ARGUMENT.
 int workspace(size_t bytes, void** out, hipStream_t st);
+// A second buffer per (device, stream) under the same rules, for operands
+// staged in a new layout before a call that itself takes workspace() (the two
+// never alias). Not available under FixedWorkspace.
+int staging_workspace(size_t bytes, void** out, hipStream_t st);
 
 // Compute units of the current device (256 if the query fails).
 int device_cus();

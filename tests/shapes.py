@@ -74,6 +74,15 @@ CONV2D_EDGE = [
     ("e06", 2, 24, 12, 16, 40, 1, 7, 1, 0),
     ("e07", 2, 8, 6, 6, 8, 3, 3, 1, 2),
     ("e08", 1, 65, 9, 9, 129, 3, 3, 2, 1),
+    # rows that are not a multiple of 4 floats: the band and row-streaming
+    # kernels on copies widened with zero columns (X for the forward, dY for
+    # dX, both for dW)
+    ("e09", 2, 64, 14, 14, 64, 3, 3, 1, 1),    # 14x14 (a ResNet stage)
+    ("e10", 2, 256, 7, 7, 48, 3, 3, 1, 1),     # 7x7, 8 channel chunks, partial filter tile
+    ("e11", 2, 128, 28, 28, 64, 3, 3, 2, 1),   # stride 2: dY rows of 14
+    ("e12", 3, 16, 11, 13, 24, 3, 3, 1, 1),    # odd height and width
+    ("e13", 2, 8, 15, 18, 8, 5, 5, 2, 2),      # 5x5 stride 2: 9-column output
+    ("e14", 2, 24, 10, 10, 16, 3, 3, 1, 0),    # no padding: 8-column output from 10
 ]
 
 # Stride-2 shapes for the four-phase and column-parity kernels (not from the
@@ -131,13 +140,16 @@ CONVT = [
 
 # Transposed shapes for the four-phase kernel (not from the reference's
 # tests): one and three input-channel chunks, 36 phase columns (two column
-# tiles), 40 output channels (a partial 32-filter tile), a 2x2 kernel.
+# tiles), 40 output channels (a partial 32-filter tile), a 2x2 kernel; and
+# input rows of 7 and 9 columns (the widened-copy path).
 CONVT_PHASE2 = [
     ("u01", 2, 32, 6, 20, 40, 4, 4, 2, 1),
     ("u02", 2, 96, 10, 36, 24, 4, 4, 2, 1),
     ("u03", 3, 64, 8, 8, 16, 2, 2, 2, 0),
     ("u04", 1, 128, 28, 28, 64, 4, 4, 2, 1),   # one image of config 5
     ("u05", 2, 96, 14, 20, 32, 4, 4, 2, 1),    # dX by column-parity streaming, one chunk
+    ("u06", 2, 64, 7, 7, 32, 4, 4, 2, 1),      # 7-column input rows (widened copy)
+    ("u07", 2, 32, 5, 9, 16, 3, 3, 2, 1),      # 3x3 s2, odd widths both ways
 ]
 
 # (M, K, N, Nbatch): Testing/test_2.py:372-375, Testing/test_14.py:148-183,
