@@ -49,6 +49,9 @@ struct WStreamArgs {
     int B, C, H, W, F, Ho, Wo, R, S, ph, pw;
     int L, nstrip, nsplit, nctile;
     int ncol;            // column tiles per row (Wo > 64: tiles of Wp = 64 output columns)
+    int vP;              // > 0: strips run over all images as one sequence of vP = Ho + R - 1
+                         // rows per image (rows Ho.. of each: dY zero); 0: strips of one image
+    int vrows;           // B * vP
     int Wp;              // padded row length of a column tile (pixels, multiple of 32)
     int rs;              // LDS row stride in halves (Wp + 16: 2 mod 4 16-byte slots)
     int NR;              // X ring rows (2*kG + R - 1)
@@ -124,11 +127,11 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int split = blockIdx.x, ty = blockIdx.y;
     const int bs = split / a.ncol, ct = split - bs * a.ncol;
-    const int b = bs / a.nstrip, strip = bs - b * a.nstrip;
+    const int b = a.vP ? 0 : bs / a.nstrip, strip = bs - b * a.nstrip;
     const int wc0 = ct * a.Wp;                   // first output column of the tile
     const int ftile = ty / a.nctile, ctile = ty - ftile * a.nctile;
-    const int ohA = strip * a.L;
-    const int Lb = min(a.L, a.Ho - ohA);         // output rows of this strip
+    const int ohA = strip * a.L;                 // first output row (virtual row with vP)
+    const int Lb = min(a.L, (a.vP ? a.vrows : a.Ho) - ohA);  // output rows of this strip
     const int nsteps = (Lb + kG - 1) / kG;
     const int xplane = kTile * a.rs;             // halves per X ring row
     half_t* const xr = smem;                     // [NR][64 c][rs]
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         xch[k] = rest % kTile;
         xrow[k] = it < kG * kTile * nxo ? rest / kTile : kG;
         xcol[k] = wc0 + 8 * j - a.pw - dd;
-        xoff[k] = ((xch[k] * a.H + xrow[k]) * a.W + xcol[k]) * 4;
+        xoff[k] = (xch[k] * a.H * a.W + xcol[k]) * 4;  // row added per load
         xqm[k] = 0;
 #pragma unroll
         for (int q = 0; q < 3; ++q) xqm[k] |= (unsigned)(xcol[k] + 4 * q) < (unsigned)a.W ? 1 << q : 0;
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
         dfl[k] = rest % kTile;
         drow[k] = it < kG * kTile * ndo ? rest / kTile : kG;
         dcol[k] = wc0 + 8 * j;
-        doff[k] = ((dfl[k] * a.Ho + ohA + drow[k]) * a.Wo + dcol[k]) * 4;
+        doff[k] = (dfl[k] * a.Ho * a.Wo + dcol[k]) * 4;  // row added per load
         dqm[k] = (dcol[k] < a.Wo ? 1 : 0) | (dcol[k] + 4 < a.Wo ? 2 : 0);
     }
     floatx4 xv[kXI][3], dv[kDI][2];  // DD < 0: three aligned quads per X item
@@ -292,11 +295,17 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     // Loads of X group rows [I0, I0 + NX) and dY output rows [O0, O0 + ND).
 #define SEERA_WG_LOAD(I0, NX, O0, ND)                                                      \
     {                                                                                      \
-        const int xrb = (ih0 + (I0)) * a.W * 4;  /* image row of group row 0, in bytes */  \
         _Pragma("unroll") for (int k = 0; k < kXI; ++k) {                                  \
-            const int i = (I0) + xrow[k], ih = ih0 + i;                                    \
+            const int i = (I0) + xrow[k];                                                  \
+            int bb = 0, ih = ih0 + i;                                                      \
+            if (a.vP) {                                                                    \
+                const int u = ohA + i;  /* virtual input row */                            \
+                bb = u / a.vP;                                                             \
+                ih = u - bb * a.vP - a.ph;                                                 \
+            }                                                                              \
             const bool rok = xrow[k] < (NX) && (unsigned)i < (unsigned)need &&             \
                              (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C;            \
+            const int xrb = (bb * a.C * a.H + ih) * a.W * 4;                               \
             uint32_t xo[3];                                                                \
             _Pragma("unroll") for (int q = 0; q < 3; ++q)                                  \
                 xo[q] = rok && ((xqm[k] >> q) & 1) ? (uint32_t)(xoff[k] + xrb + 16 * q)    \
@@ -307,10 +316,15 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                 _Pragma("unroll") for (int q = 0; q < 3; ++q) xv[k][q] = buf_load4(xsrc, xo[q]); \
             }                                                                              \
         }                                                                                  \
-        const int drb = (O0) * a.Wo * 4;                                                   \
         _Pragma("unroll") for (int k = 0; k < kDI; ++k) {                                  \
             const int o = (O0) + drow[k];                                                  \
-            const bool rok = drow[k] < (ND) && o < Lb && f0 + dfl[k] < a.F;                \
+            int bb = 0, oh = ohA + o;                                                      \
+            if (a.vP) {                                                                    \
+                bb = oh / a.vP;                                                            \
+                oh -= bb * a.vP;  /* rows Ho.. of an image's period: dY zero */            \
+            }                                                                              \
+            const bool rok = drow[k] < (ND) && o < Lb && oh < a.Ho && f0 + dfl[k] < a.F;   \
+            const int drb = (bb * a.F * a.Ho + oh) * a.Wo * 4;                             \
             _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                \
                 const uint32_t off = rok && ((dqm[k] >> q) & 1)                            \
                     ? (uint32_t)(doff[k] + drb + 16 * q) : kBufOOB;                        \
@@ -449,17 +463,34 @@ int stream_wgrad_partials(const float* Y, const float* X, int B, int C, int H, i
     if (img > kMaxTileSpanBytes || dimg > kMaxTileSpanBytes) return SEERA_OK;
     a.nctile = (C + kTile - 1) / kTile;
     const int ntiles = a.nctile * ((F + kTile - 1) / kTile);
+    // Short images whose one-strip-per-image blocks alone exceed two rounds
+    // of the CUs run as one sequence of Ho + R - 1 rows per image (the R - 1
+    // extra output rows read zero dY), so that a strip spans several images:
+    // a strip of one small image writes a whole 64 x 64*R*S partial for a
+    // few rows of work (7x7 at 512 channels: 604 MB of partials). Offsets
+    // then span the whole batch: it must fit a buffer resource.
+    const int ncu = device_cus();
+    a.vP = 0;
+    a.vrows = 0;
+    if (Ho <= 32 && (int64_t)B * a.ncol * ntiles > 2 * ncu &&
+        (int64_t)B * C * H * W * 4 < kMaxTileSpanBytes &&
+        (int64_t)B * F * Ho * Wo * 4 < kMaxTileSpanBytes) {
+        a.vP = Ho + R - 1;
+        a.vrows = B * a.vP;
+    }
+    const int rows = a.vP ? a.vrows : Ho;     // rows a strip is cut from
+    const int64_t seqs = a.vP ? 1 : B;        // row sequences
     // Strip length: fewest rounds of one block per CU, each about (steps + 2)
     // step times (the first rows arrive unhidden).
-    const int ncu = device_cus();
     double best = 1e30;
-    for (int L = kG; L < Ho + kG; L += kG) {
-        const int64_t blocks = (int64_t)B * ((Ho + L - 1) / L) * a.ncol * ntiles;
+    for (int L = kG; L < rows + kG; L += kG) {
+        const int64_t blocks = seqs * ((rows + L - 1) / L) * a.ncol * ntiles;
         const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + kG - 1) / kG + 2);
         if (cost < best) { best = cost; a.L = L; }
     }
-    a.nstrip = (Ho + a.L - 1) / a.L;
-    a.nsplit = B * a.nstrip * a.ncol;
+    a.nstrip = (rows + a.L - 1) / a.L;
+    if (seqs * a.nstrip * a.ncol > 0x7fffffff) return SEERA_OK;
+    a.nsplit = (int)(seqs * a.nstrip * a.ncol);
     // The kernel's producers reuse the rings for the bias-gradient reduction.
     if (with_db && kProd * kDI * 4 > a.lds_bytes) return SEERA_OK;
     const int nftile = (F + kTile - 1) / kTile;

@@ -59,6 +59,11 @@ CONV2D_STREAM = [
     ("s12", 1, 16, 9, 200, 24, 3, 3, 1, 1),    # 4 column tiles (64 x 3 + 8), partial filter tile
     ("s13", 2, 16, 6, 144, 16, 1, 3, 1, 1),    # 1x3: no halo rows, 3 column tiles
     ("s14", 1, 72, 5, 68, 8, 3, 3, 1, 1),      # 2 column tiles (64 + 4), 2 channel tiles
+    # many small images (images x tiles > two rounds of 256 CUs): the dW
+    # strips run across image boundaries
+    ("s15", 65, 128, 4, 4, 256, 3, 3, 1, 1),   # 8 tiles, rows of 4 + 2 per image
+    ("s16", 130, 64, 5, 8, 256, 3, 3, 1, 1),   # odd image height
+    ("s17", 520, 16, 3, 8, 16, 1, 3, 1, 1),    # 1x3: no extra rows per image
 ]
 
 # Edge shapes (not from the reference's tests): 1x1 image and kernel, channel

@@ -145,6 +145,7 @@ BWD_BIAS = [
     ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),
     ("fused_odd", 3, 64, 13, 28, 64, 3, 1, 1),            # one-pass dX + dW + db, odd rows
     ("stream_wide", 2, 32, 9, 136, 40, 3, 1, 1),          # dW + db in 3 column tiles
+    ("stream_many", 130, 32, 6, 8, 256, 3, 1, 1),         # strips across image boundaries
 ]
 
 
