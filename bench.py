@@ -521,6 +521,44 @@ def traffic_from_profiles():
     return None
 
 
+# Conv2D layer shapes beyond config 4 (N, C, H, W, F, K, stride, pad): the
+# stages of a ResNet-style network (56/28/14/7 pixels at 64..512 channels,
+# stride-2 downsampling, 1x1 projections, the 7x7 stem) and wide rows.
+CONV_LAYERS = [
+    (64, 128, 28, 28, 128, 3, 1, 1), (64, 256, 14, 14, 256, 3, 1, 1),
+    (64, 512, 7, 7, 512, 3, 1, 1), (64, 64, 56, 56, 128, 3, 2, 1),
+    (64, 128, 28, 28, 256, 3, 2, 1), (64, 256, 56, 56, 64, 1, 1, 0),
+    (64, 64, 56, 56, 256, 1, 1, 0), (32, 3, 224, 224, 64, 7, 2, 3),
+    (32, 64, 112, 112, 64, 3, 1, 1), (16, 128, 112, 112, 128, 3, 1, 1),
+]
+
+
+def bench_conv_layers(steps, warmup, stream):
+    """Forward and backward (dX + dW) time of each CONV_LAYERS shape on
+    uniform synthetic data: {"NxCxHxW->F kKsSpP": [ms_fwd, ms_bwd], ...}."""
+    r = np.random.default_rng(3)
+    lib = capi.load()
+    out = {}
+    for (N, C, H, W, F, K, S, P) in CONV_LAYERS:
+        Ho, Wo = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
+        x = r.uniform(-1, 1, (N, C, H, W)).astype(np.float32)
+        w = r.uniform(-0.05, 0.05, (F, C, K, K)).astype(np.float32)
+        dy = r.uniform(-1, 1, (N, F, Ho, Wo)).astype(np.float32)
+        bufs = [DeviceBuffer.from_array(v) for v in (x, w, dy)]
+        bufs += [DeviceBuffer(dy.nbytes), DeviceBuffer(x.nbytes), DeviceBuffer(w.nbytes)]
+        px, pw, pdy, py, pdx, pdw = (b.ptr for b in bufs)
+        # argument order of the reference: forward (pad, stride), backward (stride, pad)
+        fwd = lambda: capi.check(lib.seera_hip_conv2d_fwd_async(  # noqa: E731
+            px, pw, py, N, C, H, W, F, K, K, P, P, S, S, stream.ptr))
+        bwd = lambda: capi.check(lib.seera_hip_conv2d_bwd_async(  # noqa: E731
+            pw, px, pdy, pdx, pdw, N, C, H, W, F, K, K, S, S, P, P, stream.ptr))
+        key = f"{N}x{C}x{H}x{W}->{F} k{K}s{S}p{P}"
+        out[key] = [round(timed(fwd, steps, warmup, stream), 4), round(timed(bwd, steps, warmup, stream), 4)]
+        for b in bufs:
+            b.close()
+    return out
+
+
 # Single workloads for the per-kernel rocprofv3 passes (bench.py --workload NAME).
 WORKLOADS = {
     "gemm1024": lambda steps, warmup, st: bench_gemm(1024, steps, warmup, st, True),
@@ -529,6 +567,7 @@ WORKLOADS = {
     "gemm8192": lambda steps, warmup, st: bench_gemm(8192, steps, warmup, st, False),
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,
+    "conv_layers": bench_conv_layers,
     "convT_cfg5": bench_convT,
     "maxpool_2x2_s2": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 2, 2, 0),
     "maxpool_3x3_s2_p1": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 3, 2, 1),
@@ -593,7 +632,7 @@ def main():
         stream = Stream()
         res = WORKLOADS[args.workload](args.steps, args.warmup, stream)
         print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup,
-                          **{k: v for k, v in res.items() if isinstance(v, (int, float, str))}}))
+                          **{k: v for k, v in res.items() if isinstance(v, (int, float, str, list))}}))
         return
 
     stream = Stream()
