@@ -559,6 +559,29 @@ def bench_conv_layers(steps, warmup, stream):
     return out
 
 
+def bench_library_fp16_gemm(steps, warmup, stream, n=4096):
+    """The vendor library's fp16-operand GEMM (torch.matmul -> hipBLASLt, fp16
+    in and out) at n^3, timed the same way: a yardstick for the clock and MFMA
+    counters of this library's fp32-operand kernel, not part of the product."""
+    import torch
+
+    r = np.random.default_rng(n)
+    a = torch.from_numpy(r.uniform(-1, 1, (n, n)).astype(np.float16)).cuda()
+    b = torch.from_numpy(r.uniform(-1, 1, (n, n)).astype(np.float16)).cuda()
+    for _ in range(warmup):
+        c = a @ b
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        c = a @ b
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    del c
+    return {"ms": ms, "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12}
+
+
 # Single workloads for the per-kernel rocprofv3 passes (bench.py --workload NAME).
 WORKLOADS = {
     "gemm1024": lambda steps, warmup, st: bench_gemm(1024, steps, warmup, st, True),
@@ -568,6 +591,7 @@ WORKLOADS = {
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,
     "conv_layers": bench_conv_layers,
+    "library_fp16_gemm4096": bench_library_fp16_gemm,
     "convT_cfg5": bench_convT,
     "maxpool_2x2_s2": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 2, 2, 0),
     "maxpool_3x3_s2_p1": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 3, 2, 1),
@@ -622,6 +646,14 @@ def main():
               "(the GEMM/conv hot path is single-device; see DESIGN.md for how it would shard)",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload and args.workload.startswith("library_"):
+        # The vendor-library yardstick runs on torch alone, before this
+        # library touches HIP: torch's bundled HIP runtime sees no device in a
+        # process where the system runtime has already opened it.
+        res = WORKLOADS[args.workload](args.steps, args.warmup, None)
+        print(json.dumps({"workload": args.workload, "steps": args.steps, "warmup": args.warmup,
+                          **res}))
+        return
     if not capi.gpu_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
