@@ -88,6 +88,10 @@ CONV2D_EDGE = [
     ("e12", 3, 16, 11, 13, 24, 3, 3, 1, 1),    # odd height and width
     ("e13", 2, 8, 15, 18, 8, 5, 5, 2, 2),      # 5x5 stride 2: 9-column output
     ("e14", 2, 24, 10, 10, 16, 3, 3, 1, 0),    # no padding: 8-column output from 10
+    # 1x1 stride 1 beside 3x3 layers of the same stages (projections)
+    ("k01", 3, 256, 14, 14, 64, 1, 1, 1, 0),   # 14-column rows, 256 channels
+    ("k02", 2, 64, 7, 8, 256, 1, 1, 1, 0),     # 256 filters
+    ("k03", 2, 30, 6, 10, 18, 1, 1, 1, 0),     # channels not a multiple of 8
 ]
 
 # Stride-2 shapes for the four-phase and column-parity kernels (not from the

@@ -31,6 +31,7 @@ SHAPES = [
     ("band_2x2s2", 4, 32, 32, 32, 64, 2, 2, 0),    # 4 taps, small band
     ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),      # width % 4 != 0: gather GEMM
     ("gather_1f", 4, 8, 9, 9, 1, 3, 1, 1),         # one filter
+    ("conv1x1", 3, 32, 10, 12, 24, 1, 1, 0),       # 1x1 projection
 ]
 
 
