@@ -279,6 +279,103 @@ int widen_all(int n, const float* const* in, const int64_t* rows, const int* W, 
     return SEERA_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Space-to-depth form of a stride-2 convolution with a large kernel (the 7x7
+// stem on 3 channels): the input's 2x2 pixel blocks become 4C channels and the
+// kernel's taps (2t + dy, 2u + dx) become channel (c, dy, dx) of a T2 x U2 =
+// ceil(R/2) x ceil(S/2) kernel, so that
+//   Y[b, f, oh, ow] = sum_{c2, t, u} W2[f, c2, t, u] * X2[b, c2, oh + t, ow + u]
+// with X2[b, (c*2 + dy)*2 + dx, i, j] = X[b, c, 2i + dy - ph, 2j + dx - pw]
+// (0 outside X) and W2[f, (c*2 + dy)*2 + dx, t, u] = W[f, c, 2t + dy, 2u + dx]
+// (0 past the kernel): a stride-1, pad-0 convolution of at most 16 taps,
+// which the band kernels take. dX and dW map back through the same index
+// maps (every X and W element has exactly one image in X2 / W2).
+// ---------------------------------------------------------------------------
+struct S2dGeom {
+    int C2, H2, W2, Wp2, T2, U2;  // X2 is [B, C2, H2, Wp2]: columns W2.. zero
+};
+
+S2dGeom s2d_geom(int C, int R, int S, int Ho, int Wo) {
+    S2dGeom g;
+    g.C2 = 4 * C;
+    g.T2 = (R + 1) / 2;
+    g.U2 = (S + 1) / 2;
+    g.H2 = Ho + g.T2 - 1;
+    g.W2 = Wo + g.U2 - 1;
+    g.Wp2 = (g.W2 + 3) & ~3;
+    return g;
+}
+
+__global__ __launch_bounds__(256) void s2d_input(const float* __restrict__ X, float* __restrict__ X2,
+                                                 int B, int C, int H, int W, int ph, int pw, int H2,
+                                                 int W2, int Wp2) {
+    const int64_t n = (int64_t)B * 4 * C * H2 * Wp2;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int j = (int)(e % Wp2);
+        int64_t r = e / Wp2;
+        const int i = (int)(r % H2);
+        r /= H2;
+        const int c2 = (int)(r % (4 * C));
+        const int64_t b = r / (4 * C);
+        const int c = c2 >> 2, dy = (c2 >> 1) & 1, dx = c2 & 1;
+        const int h = 2 * i + dy - ph, w = 2 * j + dx - pw;
+        float v = 0.f;
+        if (j < W2 && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
+            v = X[((b * C + c) * H + h) * W + w];
+        X2[e] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void s2d_weights(const float* __restrict__ Wt, float* __restrict__ W2,
+                                                   int F, int C, int R, int S, int T2, int U2) {
+    const int n = F * 4 * C * T2 * U2;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int u = e % U2, t = (e / U2) % T2, c2 = (e / (U2 * T2)) % (4 * C), f = e / (U2 * T2 * 4 * C);
+    const int c = c2 >> 2, r = 2 * t + ((c2 >> 1) & 1), q = 2 * u + (c2 & 1);
+    W2[e] = r < R && q < S ? Wt[((f * C + c) * R + r) * S + q] : 0.f;
+}
+
+// dX[b, c, h, w] = dX2[b, (c*2 + dy)*2 + dx, i, j] with 2i + dy = h + ph, 2j + dx = w + pw.
+__global__ __launch_bounds__(256) void d2s_input(const float* __restrict__ dX2, float* __restrict__ dX,
+                                                 int B, int C, int H, int W, int ph, int pw, int H2,
+                                                 int W2) {
+    const int64_t n = (int64_t)B * C * H * W;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int w = (int)(e % W);
+        int64_t r = e / W;
+        const int h = (int)(r % H);
+        const int64_t bc = r / H;  // b * C + c
+        const int c = (int)(bc % C);
+        const int64_t b = bc / C;
+        const int pr = h + ph, pc = w + pw;
+        const int c2 = (c * 2 + (pr & 1)) * 2 + (pc & 1);
+        const int i = pr >> 1, j = pc >> 1;
+        dX[e] = i < H2 && j < W2 ? dX2[((b * 4 * C + c2) * H2 + i) * W2 + j] : 0.f;
+    }
+}
+
+// dW[f, c, r, s] = dW2[f, (c*2 + r%2)*2 + s%2, r/2, s/2].
+__global__ __launch_bounds__(256) void d2s_weights(const float* __restrict__ dW2, float* __restrict__ dW,
+                                                   int F, int C, int R, int S, int T2, int U2) {
+    const int n = F * C * R * S;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int q = e % S, r = (e / S) % R, c = (e / (S * R)) % C, f = e / (S * R * C);
+    const int c2 = (c * 2 + (r & 1)) * 2 + (q & 1);
+    dW[e] = dW2[((f * 4 * C + c2) * T2 + (r >> 1)) * U2 + (q >> 1)];
+}
+
+// Whether a stride-2 convolution takes the space-to-depth form: a kernel with
+// more taps than the direct band kernels hold (16) whose halves fit them.
+bool s2d_applies(int R, int S, int sh, int sw) {
+    return sh == 2 && sw == 2 && R * S > 16 && ((R + 1) / 2) * ((S + 1) / 2) <= 16;
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 8192); }
+
 }  // namespace
 
 namespace {
@@ -294,6 +391,25 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
     bool used = false;
     SEERA_TRY(band_conv_fwd(X, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi));
     if (used) return SEERA_OK;
+    if (s2d_applies(R, S, sh, sw)) {
+        const int Ho2 = (H + 2 * ph - R) / sh + 1, Wo2 = (W + 2 * pw - S) / sw + 1;
+        const S2dGeom g = s2d_geom(C, R, S, Ho2, Wo2);
+        const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
+        if (xn * 4 < kMaxTileSpanBytes) {
+            void* ws = nullptr;
+            SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+            float* X2 = static_cast<float*>(ws);
+            float* W2 = X2 + xn;
+            hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
+                               pw, g.H2, g.W2, g.Wp2);
+            hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wt, W2, F, C, R, S,
+                               g.T2, g.U2);
+            SEERA_HIP_TRY(hipGetLastError());
+            SEERA_TRY(band_conv_fwd(X2, W2, Y, B, g.C2, g.H2, g.W2, F, g.T2, g.U2, 1, 1, 0, 0, st,
+                                    &used, epi, g.Wp2));
+            if (used) return SEERA_OK;
+        }
+    }
     if (W % 4 != 0 && R * S <= 16) {
         // Rows that are not float4-aligned: the band path on a copy of X
         // widened to a multiple of 4 columns (zeros past W, where the
@@ -414,6 +530,28 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
         return fail(SEERA_ERR_INVALID_ARGUMENT, "conv extent exceeds int range");
     if (npix == 0 || C == 0) return SEERA_OK;
     bool used = false;
+    if (s2d_applies(R, S, sh, sw) && Wi % 4 == 0) {
+        // dX2 = the stride-1 transposed convolution of dY with W2, then back
+        // to the input's layout
+        const S2dGeom g = s2d_geom(C, R, S, Hi, Wi);
+        const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.W2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
+        void* ws = nullptr;
+        SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+        float* dX2 = static_cast<float*>(ws);
+        float* W2 = dX2 + xn;
+        hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wconv, W2, F, C, R, S,
+                           g.T2, g.U2);
+        SEERA_HIP_TRY(hipGetLastError());
+        SEERA_TRY(band_conv_dgrad(Yin, W2, dX2, B, F, Hi, Wi, g.C2, g.H2, g.W2, g.T2, g.U2, 1, 1, 0,
+                                  0, st, &used));
+        if (used) {
+            const int64_t n = (int64_t)B * C * H * W;
+            hipLaunchKernelGGL(d2s_input, dim3(grid_for(n)), dim3(256), 0, st, dX2, out, B, C, H, W,
+                               ph, pw, g.H2, g.W2);
+            SEERA_HIP_TRY(hipGetLastError());
+            return SEERA_OK;
+        }
+    }
     SEERA_TRY(band_conv_dgrad(Yin, Wconv, out, B, F, Hi, Wi, C, H, W, R, S, sh, sw, ph, pw, st,
                               &used));
     if (used) return SEERA_OK;
@@ -489,6 +627,28 @@ int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int 
     bool used = false, db_done = false;
     SEERA_TRY(band_conv_wgrad(Y, X, dW, db, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used,
                               &db_done));
+    if (!used && s2d_applies(R, S, sh, sw) && Wo % 4 == 0) {
+        // dW2 = the stride-1 dW of (dY, X2), then back to W's layout
+        const S2dGeom g = s2d_geom(C, R, S, Ho, Wo);
+        const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
+        if (xn * 4 < kMaxTileSpanBytes) {
+            void* ws = nullptr;
+            SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+            float* X2 = static_cast<float*>(ws);
+            float* dW2 = X2 + xn;
+            hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
+                               pw, g.H2, g.W2, g.Wp2);
+            SEERA_HIP_TRY(hipGetLastError());
+            SEERA_TRY(band_conv_wgrad(Y, X2, dW2, nullptr, B, g.C2, g.H2, g.Wp2, F, g.T2, g.U2, 1, 1,
+                                      0, 0, st, &used, &db_done, Wo));
+            if (used) {
+                const int n = F * C * R * S;
+                hipLaunchKernelGGL(d2s_weights, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                                   dW2, dW, F, C, R, S, g.T2, g.U2);
+                SEERA_HIP_TRY(hipGetLastError());
+            }
+        }
+    }
     if (!used && (W % 4 != 0 || Wo % 4 != 0)) {
         // Rows that are not float4-aligned: the band / row-streaming dW on
         // copies of X and dY widened with zero columns to a width W2 >= W

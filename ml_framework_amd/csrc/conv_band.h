@@ -156,8 +156,10 @@ int wgrad_s2_partials(const float* Y, const float* X, int B, int C, int H, int W
 // X[b, c, oh*sh - ph + r, ow*sw - pw + s], when the band path applies. With a
 // non-null db and the row-streaming path, also db[f] = sum of dY[b, f, ...]
 // from the same pass (*db_done reports it; otherwise the caller computes db).
+// wo_override > 0: dY rows hold that many columns, fewer than W's geometry
+// gives (X's rows are a widened copy: W is their pitch).
 int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H,
                     int W, int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st,
-                    bool* used, bool* db_done);
+                    bool* used, bool* db_done, int wo_override = 0);
 
 }  // namespace seera

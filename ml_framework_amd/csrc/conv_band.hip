@@ -1175,11 +1175,13 @@ int band_conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int
 
 int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int C, int H,
                     int W, int F, int R, int S, int sh, int sw, int ph, int pw, hipStream_t st,
-                    bool* used, bool* db_done) {
+                    bool* used, bool* db_done, int wo_override) {
     *used = false;
     *db_done = false;
-    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = (W + 2 * pw - S) / sw + 1;
-    if (sh == 1 && sw == 1) {
+    const int Wo_nat = (W + 2 * pw - S) / sw + 1;
+    const int Ho = (H + 2 * ph - R) / sh + 1, Wo = wo_override > 0 ? wo_override : Wo_nat;
+    if (Wo > Wo_nat) return SEERA_OK;  // an output column would read past X's pitch
+    if (sh == 1 && sw == 1 && Wo == Wo_nat) {
         WgradPartials wp{};
         bool streamed = false;
         SEERA_TRY(stream_wgrad_partials(Y, X, B, C, H, W, F, R, S, ph, pw, db != nullptr, st, &wp,
@@ -1227,7 +1229,10 @@ int band_conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B,
     // producer loads fit the per-thread budgets and whose two LDS stages fit.
     const int oct = sw == 1 ? 4 : 2;  // octets per X item (XItem<sw>::OCT)
     const int wo_cap = std::min(Wo, 224);
-    const int wc_opts[2] = {(wo_cap + 7) & ~7, (wo_cap + 31) & ~31};
+    // Tile widths: the whole (capped) row, or 64 / 32 columns when S shifted
+    // copies of a whole row do not fit (large S on wide rows).
+    const int wc_opts[4] = {(wo_cap + 7) & ~7, (wo_cap + 31) & ~31, std::min(64, (wo_cap + 31) & ~31),
+                            32};
     int best_px = 0;
     WgradArgs best = a;
     for (int wc : wc_opts) {

@@ -92,6 +92,11 @@ CONV2D_EDGE = [
     ("k01", 3, 256, 14, 14, 64, 1, 1, 1, 0),   # 14-column rows, 256 channels
     ("k02", 2, 64, 7, 8, 256, 1, 1, 1, 0),     # 256 filters
     ("k03", 2, 30, 6, 10, 18, 1, 1, 1, 0),     # channels not a multiple of 8
+    # stride 2 with more than 16 taps: the space-to-depth form (4C channels,
+    # ceil(R/2) x ceil(S/2) taps, stride 1)
+    ("d01", 2, 3, 20, 24, 8, 7, 7, 2, 3),      # a 7x7 stem: all three passes in that form
+    ("d02", 2, 5, 17, 21, 16, 5, 5, 2, 2),     # 5x5, 11-column output: forward only
+    ("d03", 1, 20, 12, 16, 70, 7, 7, 2, 3),    # 80 channels in that form (3 chunks), 2 filter tiles
 ]
 
 # Stride-2 shapes for the four-phase and column-parity kernels (not from the

@@ -32,6 +32,7 @@ SHAPES = [
     ("gather_w10", 2, 3, 10, 10, 4, 5, 2, 2),      # width % 4 != 0: gather GEMM
     ("gather_1f", 4, 8, 9, 9, 1, 3, 1, 1),         # one filter
     ("conv1x1", 3, 32, 10, 12, 24, 1, 1, 0),       # 1x1 projection
+    ("s2d_7x7", 2, 3, 16, 16, 8, 7, 2, 3),         # 7x7 s2: space-to-depth form
 ]
 
 
@@ -147,6 +148,7 @@ BWD_BIAS = [
     ("fused_odd", 3, 64, 13, 28, 64, 3, 1, 1),            # one-pass dX + dW + db, odd rows
     ("stream_wide", 2, 32, 9, 136, 40, 3, 1, 1),          # dW + db in 3 column tiles
     ("stream_many", 130, 32, 6, 8, 256, 3, 1, 1),         # strips across image boundaries
+    ("s2d_stem", 2, 3, 20, 24, 8, 7, 2, 3),               # 7x7 s2 in space-to-depth form
 ]
 
 
