@@ -292,12 +292,14 @@ int widen_all(int n, const float* const* in, const int64_t* rows, const int* W, 
 // maps (every X and W element has exactly one image in X2 / W2).
 // ---------------------------------------------------------------------------
 struct S2dGeom {
-    int C2, H2, W2, Wp2, T2, U2;  // X2 is [B, C2, H2, Wp2]: columns W2.. zero
+    int C2, H2, W2, Wp2, T2, U2;  // X2 is [B, C2, H2, Wp2]: channels 4C.., columns W2.. zero
 };
 
+// Channels rounded up to a multiple of 8 and rows to a multiple of 4 floats:
+// the shapes the row-streaming kernels take.
 S2dGeom s2d_geom(int C, int R, int S, int Ho, int Wo) {
     S2dGeom g;
-    g.C2 = 4 * C;
+    g.C2 = (4 * C + 7) & ~7;
     g.T2 = (R + 1) / 2;
     g.U2 = (S + 1) / 2;
     g.H2 = Ho + g.T2 - 1;
@@ -307,40 +309,41 @@ S2dGeom s2d_geom(int C, int R, int S, int Ho, int Wo) {
 }
 
 __global__ __launch_bounds__(256) void s2d_input(const float* __restrict__ X, float* __restrict__ X2,
-                                                 int B, int C, int H, int W, int ph, int pw, int H2,
-                                                 int W2, int Wp2) {
-    const int64_t n = (int64_t)B * 4 * C * H2 * Wp2;
+                                                 int B, int C, int H, int W, int ph, int pw, int C2,
+                                                 int H2, int W2, int Wp2) {
+    const int64_t n = (int64_t)B * C2 * H2 * Wp2;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
          e += (int64_t)gridDim.x * blockDim.x) {
         const int j = (int)(e % Wp2);
         int64_t r = e / Wp2;
         const int i = (int)(r % H2);
         r /= H2;
-        const int c2 = (int)(r % (4 * C));
-        const int64_t b = r / (4 * C);
+        const int c2 = (int)(r % C2);
+        const int64_t b = r / C2;
         const int c = c2 >> 2, dy = (c2 >> 1) & 1, dx = c2 & 1;
         const int h = 2 * i + dy - ph, w = 2 * j + dx - pw;
         float v = 0.f;
-        if (j < W2 && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
+        if (c < C && j < W2 && (unsigned)h < (unsigned)H && (unsigned)w < (unsigned)W)
             v = X[((b * C + c) * H + h) * W + w];
         X2[e] = v;
     }
 }
 
 __global__ __launch_bounds__(256) void s2d_weights(const float* __restrict__ Wt, float* __restrict__ W2,
-                                                   int F, int C, int R, int S, int T2, int U2) {
-    const int n = F * 4 * C * T2 * U2;
+                                                   int F, int C, int R, int S, int C2, int T2, int U2) {
+    const int n = F * C2 * T2 * U2;
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n) return;
-    const int u = e % U2, t = (e / U2) % T2, c2 = (e / (U2 * T2)) % (4 * C), f = e / (U2 * T2 * 4 * C);
+    const int u = e % U2, t = (e / U2) % T2, c2 = (e / (U2 * T2)) % C2, f = e / (U2 * T2 * C2);
     const int c = c2 >> 2, r = 2 * t + ((c2 >> 1) & 1), q = 2 * u + (c2 & 1);
-    W2[e] = r < R && q < S ? Wt[((f * C + c) * R + r) * S + q] : 0.f;
+    W2[e] = c < C && r < R && q < S ? Wt[((f * C + c) * R + r) * S + q] : 0.f;
 }
 
-// dX[b, c, h, w] = dX2[b, (c*2 + dy)*2 + dx, i, j] with 2i + dy = h + ph, 2j + dx = w + pw.
+// dX[b, c, h, w] = dX2[b, (c*2 + dy)*2 + dx, i, j] with 2i + dy = h + ph, 2j + dx = w + pw
+// (dX2 is [B, C2, H2, W2]).
 __global__ __launch_bounds__(256) void d2s_input(const float* __restrict__ dX2, float* __restrict__ dX,
-                                                 int B, int C, int H, int W, int ph, int pw, int H2,
-                                                 int W2) {
+                                                 int B, int C, int H, int W, int ph, int pw, int C2,
+                                                 int H2, int W2) {
     const int64_t n = (int64_t)B * C * H * W;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
          e += (int64_t)gridDim.x * blockDim.x) {
@@ -353,19 +356,19 @@ __global__ __launch_bounds__(256) void d2s_input(const float* __restrict__ dX2, 
         const int pr = h + ph, pc = w + pw;
         const int c2 = (c * 2 + (pr & 1)) * 2 + (pc & 1);
         const int i = pr >> 1, j = pc >> 1;
-        dX[e] = i < H2 && j < W2 ? dX2[((b * 4 * C + c2) * H2 + i) * W2 + j] : 0.f;
+        dX[e] = i < H2 && j < W2 ? dX2[((b * C2 + c2) * H2 + i) * W2 + j] : 0.f;
     }
 }
 
-// dW[f, c, r, s] = dW2[f, (c*2 + r%2)*2 + s%2, r/2, s/2].
+// dW[f, c, r, s] = dW2[f, (c*2 + r%2)*2 + s%2, r/2, s/2] (dW2 is [F, C2, T2, U2]).
 __global__ __launch_bounds__(256) void d2s_weights(const float* __restrict__ dW2, float* __restrict__ dW,
-                                                   int F, int C, int R, int S, int T2, int U2) {
+                                                   int F, int C, int R, int S, int C2, int T2, int U2) {
     const int n = F * C * R * S;
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n) return;
     const int q = e % S, r = (e / S) % R, c = (e / (S * R)) % C, f = e / (S * R * C);
     const int c2 = (c * 2 + (r & 1)) * 2 + (q & 1);
-    dW[e] = dW2[((f * 4 * C + c2) * T2 + (r >> 1)) * U2 + (q >> 1)];
+    dW[e] = dW2[((f * C2 + c2) * T2 + (r >> 1)) * U2 + (q >> 1)];
 }
 
 // Whether a stride-2 convolution takes the space-to-depth form: a kernel with
@@ -401,9 +404,9 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
             float* X2 = static_cast<float*>(ws);
             float* W2 = X2 + xn;
             hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
-                               pw, g.H2, g.W2, g.Wp2);
+                               pw, g.C2, g.H2, g.W2, g.Wp2);
             hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wt, W2, F, C, R, S,
-                               g.T2, g.U2);
+                               g.C2, g.T2, g.U2);
             SEERA_HIP_TRY(hipGetLastError());
             SEERA_TRY(band_conv_fwd(X2, W2, Y, B, g.C2, g.H2, g.W2, F, g.T2, g.U2, 1, 1, 0, 0, st,
                                     &used, epi, g.Wp2));
@@ -533,21 +536,23 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
     if (s2d_applies(R, S, sh, sw) && Wi % 4 == 0) {
         // dX2 = the stride-1 transposed convolution of dY with W2, then back
         // to the input's layout
+        // (dX2 is computed Wp2 columns wide: the columns past W2 read only dY
+        // positions past its edge, and are never read back)
         const S2dGeom g = s2d_geom(C, R, S, Hi, Wi);
-        const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.W2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
+        const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
         void* ws = nullptr;
         SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
         float* dX2 = static_cast<float*>(ws);
         float* W2 = dX2 + xn;
         hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wconv, W2, F, C, R, S,
-                           g.T2, g.U2);
+                           g.C2, g.T2, g.U2);
         SEERA_HIP_TRY(hipGetLastError());
-        SEERA_TRY(band_conv_dgrad(Yin, W2, dX2, B, F, Hi, Wi, g.C2, g.H2, g.W2, g.T2, g.U2, 1, 1, 0,
+        SEERA_TRY(band_conv_dgrad(Yin, W2, dX2, B, F, Hi, Wi, g.C2, g.H2, g.Wp2, g.T2, g.U2, 1, 1, 0,
                                   0, st, &used));
         if (used) {
             const int64_t n = (int64_t)B * C * H * W;
             hipLaunchKernelGGL(d2s_input, dim3(grid_for(n)), dim3(256), 0, st, dX2, out, B, C, H, W,
-                               ph, pw, g.H2, g.W2);
+                               ph, pw, g.C2, g.H2, g.Wp2);
             SEERA_HIP_TRY(hipGetLastError());
             return SEERA_OK;
         }
@@ -637,14 +642,14 @@ int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int 
             float* X2 = static_cast<float*>(ws);
             float* dW2 = X2 + xn;
             hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
-                               pw, g.H2, g.W2, g.Wp2);
+                               pw, g.C2, g.H2, g.W2, g.Wp2);
             SEERA_HIP_TRY(hipGetLastError());
             SEERA_TRY(band_conv_wgrad(Y, X2, dW2, nullptr, B, g.C2, g.H2, g.Wp2, F, g.T2, g.U2, 1, 1,
                                       0, 0, st, &used, &db_done, Wo));
             if (used) {
                 const int n = F * C * R * S;
                 hipLaunchKernelGGL(d2s_weights, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                   dW2, dW, F, C, R, S, g.T2, g.U2);
+                                   dW2, dW, F, C, R, S, g.C2, g.T2, g.U2);
                 SEERA_HIP_TRY(hipGetLastError());
             }
         }
