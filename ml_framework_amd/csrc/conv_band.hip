@@ -277,11 +277,17 @@ bool plan_tile(BandConvArgs& a) {
         max_u = std::max(max_u, a.ph[z].U);
     }
     a.WC = std::min(max_wo, 224);
-    for (a.TH = std::max(1, std::min(max_ho, 224 / a.WC)); a.TH >= 1; --a.TH) {
-        a.BR = (a.TH - 1) * a.ish + std::max(max_t, 1);
-        a.BC4 = ((a.WC - 1) * a.isw + std::max(max_u, 1) + 3 + 3) & ~3;
-        a.lds_bytes = (int64_t)a.max_taps * 2048 * 2 + (int64_t)a.BR * a.BC4 * 64;
-        if (a.lds_bytes <= kBandMaxLds) break;
+    // The tallest tile whose band fits half the LDS (two blocks per CU: one
+    // block's loads run under the other's taps; 3x3 s2 64 -> 128 at 56^2
+    // forward 61 -> 50 us), else the whole LDS.
+    for (int cap : {kBandMaxLds / 2, kBandMaxLds}) {
+        for (a.TH = std::max(1, std::min(max_ho, 224 / a.WC)); a.TH >= 1; --a.TH) {
+            a.BR = (a.TH - 1) * a.ish + std::max(max_t, 1);
+            a.BC4 = ((a.WC - 1) * a.isw + std::max(max_u, 1) + 3 + 3) & ~3;
+            a.lds_bytes = (int64_t)a.max_taps * 2048 * 2 + (int64_t)a.BR * a.BC4 * 64;
+            if (a.lds_bytes <= cap) break;
+        }
+        if (a.TH >= 1) break;
     }
     if (a.TH < 1) return false;
     for (int z = 0, blocks = 0; z < a.nphase; ++z) {
