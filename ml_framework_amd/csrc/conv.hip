@@ -256,15 +256,31 @@ __global__ __launch_bounds__(256) void widen_rows(const float* __restrict__ in,
     }
 }
 
+// A staging buffer for a re-laid-out operand; *got is false (and nothing is
+// reported) when the device is out of memory for it, so that the caller takes
+// the path that needs no copy.
+int stage(size_t bytes, void** out, hipStream_t st, bool* got) {
+    *got = false;
+    const int e = staging_workspace(bytes, out, st);
+    if (e == SEERA_ERR_OUT_OF_MEMORY) {
+        clear_error();
+        return SEERA_OK;
+    }
+    SEERA_TRY(e);
+    *got = true;
+    return SEERA_OK;
+}
+
 // Copies `n` tensors of rows[i] rows x W[i] floats into one staging buffer,
 // each widened to Wp[i] (a multiple of 4) with zero columns; out[i] receives
 // the copy's address.
 int widen_all(int n, const float* const* in, const int64_t* rows, const int* W, const int* Wp,
-              float** out, hipStream_t st) {
+              float** out, hipStream_t st, bool* got) {
     size_t total = 0;
     for (int i = 0; i < n; ++i) total += ((size_t)rows[i] * Wp[i] * 4 + 255) & ~(size_t)255;
     void* ws = nullptr;
-    SEERA_TRY(staging_workspace(std::max<size_t>(total, 256), &ws, st));
+    SEERA_TRY(stage(std::max<size_t>(total, 256), &ws, st, got));
+    if (!*got) return SEERA_OK;
     char* p = static_cast<char*>(ws);
     for (int i = 0; i < n; ++i) {
         out[i] = reinterpret_cast<float*>(p);
@@ -398,9 +414,11 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
         const int Ho2 = (H + 2 * ph - R) / sh + 1, Wo2 = (W + 2 * pw - S) / sw + 1;
         const S2dGeom g = s2d_geom(C, R, S, Ho2, Wo2);
         const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
-        if (xn * 4 < kMaxTileSpanBytes) {
-            void* ws = nullptr;
-            SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+        void* ws = nullptr;
+        bool got = false;
+        if (xn * 4 < kMaxTileSpanBytes)
+            SEERA_TRY(stage(sizeof(float) * (size_t)(xn + wn), &ws, st, &got));
+        if (got) {
             float* X2 = static_cast<float*>(ws);
             float* W2 = X2 + xn;
             hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
@@ -420,9 +438,13 @@ int conv_fwd_epi(const float* X, const float* Wt, float* Y, int B, int C, int H,
         const int Wp = (W + 3) & ~3;
         const int64_t rows = (int64_t)B * C * H;
         float* Xw = nullptr;
-        SEERA_TRY(widen_all(1, &X, &rows, &W, &Wp, &Xw, st));
-        SEERA_TRY(band_conv_fwd(Xw, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi, Wp));
-        if (used) return SEERA_OK;
+        bool got = false;
+        SEERA_TRY(widen_all(1, &X, &rows, &W, &Wp, &Xw, st, &got));
+        if (got) {
+            SEERA_TRY(band_conv_fwd(Xw, Wt, Y, B, C, H, W, F, R, S, sh, sw, ph, pw, st, &used, epi,
+                                    Wp));
+            if (used) return SEERA_OK;
+        }
     }
     // Gather path: any width, any tile size.
     FwdGather g{X, C, H, W, R, S, Wo, Ho * Wo, sh, sw, ph, pw, (int)npix};
@@ -541,14 +563,17 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
         const S2dGeom g = s2d_geom(C, R, S, Hi, Wi);
         const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
         void* ws = nullptr;
-        SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+        bool got = false;
+        SEERA_TRY(stage(sizeof(float) * (size_t)(xn + wn), &ws, st, &got));
         float* dX2 = static_cast<float*>(ws);
         float* W2 = dX2 + xn;
-        hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wconv, W2, F, C, R, S,
-                           g.C2, g.T2, g.U2);
-        SEERA_HIP_TRY(hipGetLastError());
-        SEERA_TRY(band_conv_dgrad(Yin, W2, dX2, B, F, Hi, Wi, g.C2, g.H2, g.Wp2, g.T2, g.U2, 1, 1, 0,
-                                  0, st, &used));
+        if (got) {
+            hipLaunchKernelGGL(s2d_weights, dim3(grid_for(wn)), dim3(256), 0, st, Wconv, W2, F, C, R,
+                               S, g.C2, g.T2, g.U2);
+            SEERA_HIP_TRY(hipGetLastError());
+            SEERA_TRY(band_conv_dgrad(Yin, W2, dX2, B, F, Hi, Wi, g.C2, g.H2, g.Wp2, g.T2, g.U2, 1, 1,
+                                      0, 0, st, &used));
+        }
         if (used) {
             const int64_t n = (int64_t)B * C * H * W;
             hipLaunchKernelGGL(d2s_input, dim3(grid_for(n)), dim3(256), 0, st, dX2, out, B, C, H, W,
@@ -567,10 +592,13 @@ int conv_dgrad(const float* Yin, const float* Wconv, float* out, int B, int F, i
         const int Wp = (Wi + 3) & ~3;
         const int64_t rows = (int64_t)B * F * Hi;
         float* Yw = nullptr;
-        SEERA_TRY(widen_all(1, &Yin, &rows, &Wi, &Wp, &Yw, st));
-        SEERA_TRY(band_conv_dgrad(Yw, Wconv, out, B, F, Hi, Wp, C, H, W, R, S, sh, sw, ph, pw, st,
-                                  &used));
-        if (used) return SEERA_OK;
+        bool got = false;
+        SEERA_TRY(widen_all(1, &Yin, &rows, &Wi, &Wp, &Yw, st, &got));
+        if (got) {
+            SEERA_TRY(band_conv_dgrad(Yw, Wconv, out, B, F, Hi, Wp, C, H, W, R, S, sh, sw, ph, pw,
+                                      st, &used));
+            if (used) return SEERA_OK;
+        }
     }
     // Gather path: any width, any stride.
     void* ws = nullptr;
@@ -636,9 +664,11 @@ int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int 
         // dW2 = the stride-1 dW of (dY, X2), then back to W's layout
         const S2dGeom g = s2d_geom(C, R, S, Ho, Wo);
         const int64_t xn = (int64_t)B * g.C2 * g.H2 * g.Wp2, wn = (int64_t)F * g.C2 * g.T2 * g.U2;
-        if (xn * 4 < kMaxTileSpanBytes) {
-            void* ws = nullptr;
-            SEERA_TRY(staging_workspace(sizeof(float) * (size_t)(xn + wn), &ws, st));
+        void* ws = nullptr;
+        bool got = false;
+        if (xn * 4 < kMaxTileSpanBytes)
+            SEERA_TRY(stage(sizeof(float) * (size_t)(xn + wn), &ws, st, &got));
+        if (got) {
             float* X2 = static_cast<float*>(ws);
             float* dW2 = X2 + xn;
             hipLaunchKernelGGL(s2d_input, dim3(grid_for(xn)), dim3(256), 0, st, X, X2, B, C, H, W, ph,
@@ -670,9 +700,11 @@ int conv_wgrad(const float* Y, const float* X, float* dW, float* db, int B, int 
             const int64_t rows[2] = {(int64_t)B * C * H, (int64_t)B * F * Ho};
             const int w0[2] = {W, Wo}, w1[2] = {W2, Wo2};
             float* dst[2] = {nullptr, nullptr};
-            SEERA_TRY(widen_all(2, src, rows, w0, w1, dst, st));
-            SEERA_TRY(band_conv_wgrad(dst[1], dst[0], dW, db, B, C, H, W2, F, R, S, sh, sw, ph, pw,
-                                      st, &used, &db_done));
+            bool got = false;
+            SEERA_TRY(widen_all(2, src, rows, w0, w1, dst, st, &got));
+            if (got)
+                SEERA_TRY(band_conv_wgrad(dst[1], dst[0], dW, db, B, C, H, W2, F, R, S, sh, sw, ph,
+                                          pw, st, &used, &db_done));
         }
     }
     if (!used) {
