@@ -332,3 +332,48 @@ def test_convT_backward_graph(lib, stream):
     _replays_match_eager(lib, stream, seq, [(x, None), (dy, None)],
                          [(dx, (N, Ci, H, W), np.float32), (dw, (Ci, Co, 4, 4), np.float32)],
                          make_inputs)
+
+
+def test_staged_layouts_graph(lib, stream):
+    """Convolutions that stage a re-laid-out operand in the second per-stream
+    buffer: a 14x14 layer (rows widened to 16 floats for the forward, dX and
+    dW) and a 7x7 stride-2 stem (space-to-depth) forward and backward, with
+    bias and ReLU on the stem, captured and replayed."""
+    r = np.random.default_rng(5)
+    N, C, H, W, F = 4, 64, 14, 14, 64
+    x = DeviceBuffer(N * C * H * W * 4)
+    w = DeviceBuffer.from_array((r.standard_normal((F, C, 3, 3)) * 0.05).astype(np.float32))
+    y, dx = DeviceBuffer(N * F * H * W * 4), DeviceBuffer(N * C * H * W * 4)
+    dy, dw = DeviceBuffer(N * F * H * W * 4), DeviceBuffer(F * C * 9 * 4)
+    Ns, Cs, Hs, Fs = 2, 3, 32, 16  # stem: 32x32 -> 16x16
+    xs = DeviceBuffer(Ns * Cs * Hs * Hs * 4)
+    ws = DeviceBuffer.from_array((r.standard_normal((Fs, Cs, 7, 7)) * 0.1).astype(np.float32))
+    bs = DeviceBuffer.from_array(r.uniform(-0.1, 0.1, Fs).astype(np.float32))
+    ys, ms = DeviceBuffer(Ns * Fs * 16 * 16 * 4), DeviceBuffer(Ns * Fs * 16 * 16 * 4)
+    dys = DeviceBuffer(Ns * Fs * 16 * 16 * 4)
+    dxs, dws = DeviceBuffer(Ns * Cs * Hs * Hs * 4), DeviceBuffer(Fs * Cs * 49 * 4)
+
+    def seq():
+        capi.check(lib.seera_hip_conv2d_fwd_async(x.ptr, w.ptr, y.ptr, N, C, H, W, F, 3, 3, 1, 1,
+                                                  1, 1, stream))
+        capi.check(lib.seera_hip_conv2d_bwd_async(w.ptr, x.ptr, dy.ptr, dx.ptr, dw.ptr, N, C, H, W,
+                                                  F, 3, 3, 1, 1, 1, 1, stream))
+        capi.check(lib.seera_hip_conv2d_fwd_bias_act_async(
+            xs.ptr, ws.ptr, bs.ptr, ys.ptr, ms.ptr, Ns, Cs, Hs, Hs, Fs, 7, 7, 3, 3, 2, 2,
+            capi.SEERA_ACT_RELU, stream))
+        capi.check(lib.seera_hip_conv2d_bwd_async(ws.ptr, xs.ptr, dys.ptr, dxs.ptr, dws.ptr, Ns, Cs,
+                                                  Hs, Hs, Fs, 7, 7, 2, 2, 3, 3, stream))
+
+    def make_inputs(rep):
+        g = np.random.default_rng(30 + rep)
+        return [g.standard_normal((N, C, H, W)).astype(np.float32),
+                g.standard_normal((N, F, H, W)).astype(np.float32),
+                g.standard_normal((Ns, Cs, Hs, Hs)).astype(np.float32),
+                g.standard_normal((Ns, Fs, 16, 16)).astype(np.float32)]
+
+    outputs = [(y, (N, F, H, W), np.float32), (dx, (N, C, H, W), np.float32),
+               (dw, (F, C, 3, 3), np.float32), (ys, (Ns, Fs, 16, 16), np.float32),
+               (ms, (Ns, Fs, 16, 16), np.float32), (dxs, (Ns, Cs, Hs, Hs), np.float32),
+               (dws, (Fs, Cs, 7, 7), np.float32)]
+    _replays_match_eager(lib, stream, seq, [(x, None), (dy, None), (xs, None), (dys, None)],
+                         outputs, make_inputs)
