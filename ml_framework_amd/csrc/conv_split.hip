@@ -5,8 +5,10 @@
 //   out[b, f, oh, ow] = sum_{c, t, u} Wk[f, t, u, c] * in[b, c, oh + t - 1, ow + u - 1]
 // (convolution.cu:15-101 forward; convolution.cu:144-265 dX).
 //
-// A block owns one image, a strip of L output rows and 64 filters, and walks
-// the strip two output rows per step. One wave of each role per SIMD:
+// A block owns one image, a strip of L output rows, up to 56 columns (rows
+// wider than that run as column tiles, each ring row holding the tile's
+// columns and one quad of halo on either side) and 64 filters, and walks the
+// strip two output rows per step. One wave of each role per SIMD:
 //   * 4 consumer waves: wave w computes half w&1 (32 pixels) of output row
 //     w>>1 of the step for all 64 filters (v_mfma_f32_16x16x32_f16, 16 pixels
 //     x 32 channels of the ring as A, the LDS-resident weights as B; the 18
@@ -79,6 +81,7 @@ struct SplitArgs {
     float* out;          // [B, F, H, W] fp32
     int B, H, W, F;
     int L, nstrip;       // output rows per strip, strips per image
+    int ncol, Wt;        // column tiles per row, columns per tile (W > 56: tiles of <= 56)
     int nq;              // ring column quads per row (W/4 + 2)
     int nqo;             // output column quads per row (W/4)
     ConvEpi epi;
@@ -89,7 +92,9 @@ constexpr int kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2;
 template <int EPI>
 __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
-    const int strip = blockIdx.x % a.nstrip, b = blockIdx.x / a.nstrip;
+    const int ct = blockIdx.x % a.ncol, bs = blockIdx.x / a.ncol;
+    const int strip = bs % a.nstrip, b = bs / a.nstrip;
+    const int c0 = ct * a.Wt;                  // first column of the tile
     const int ftile = blockIdx.y;
     const int ohA = strip * a.L;
     const int Lb = min(a.L, a.H - ohA);        // output rows of this strip
@@ -113,7 +118,7 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     // and their fp16 write into ring slot (first row + rr) % 6.
     auto item_load = [&](int it, int i0, bool on, floatx4 (&v)[8]) {
         const int cg = it & 3, q4 = (it >> 2) % a.nq, ch = (it >> 2) / a.nq % 2;
-        const int rr = it / row_items, i = i0 + rr, hin = ohA - 1 + i, win = 4 * q4 - 4;
+        const int rr = it / row_items, i = i0 + rr, hin = ohA - 1 + i, win = c0 + 4 * q4 - 4;
         const bool ok = on && (unsigned)hin < (unsigned)a.H && (unsigned)win < (unsigned)a.W;
         const uint32_t vo = ok ? (uint32_t)((((ch * 32 + cg * 8) * a.H + hin) * a.W + win) * 4) : kBufOOB;
 #pragma unroll
@@ -270,8 +275,8 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
             for (int k = 0; k < kStoreItems; ++k) {
                 if (sf[k] < 0) continue;
                 const int o = 2 * st + sr[k], f = ftile * 64 + sf[k];
-                const uint32_t off = o < Lb && f < a.F
-                    ? (uint32_t)(((f * a.H + ohA + o) * a.W + 4 * sq[k]) * 4) : kBufOOB;
+                const uint32_t off = o < Lb && f < a.F && c0 + 4 * sq[k] < a.W
+                    ? (uint32_t)(((f * a.H + ohA + o) * a.W + c0 + 4 * sq[k]) * 4) : kBufOOB;
                 floatx4_t x = v[k];
                 if constexpr (EPI != kEpiNone) {
 #pragma unroll
@@ -314,7 +319,7 @@ int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     if (P.T != 3 || P.U != 3 || P.iph != 1 || P.ipw != 1 || P.oph != 0 || P.opw != 0 || P.woff != 0)
         return SEERA_OK;
     if (band.Hout != band.H || band.Wout != band.W || P.Ho != band.H || P.Wo != band.W) return SEERA_OK;
-    if (band.W < 4 || band.W > 56 || band.W % 4 != 0 || band.H < 1 || band.B < 1) return SEERA_OK;
+    if (band.W < 4 || band.W % 4 != 0 || band.H < 1 || band.B < 1) return SEERA_OK;
     if ((reinterpret_cast<uintptr_t>(band.out) & 15) != 0 || (reinterpret_cast<uintptr_t>(band.in) & 15) != 0)
         return SEERA_OK;
     if ((int64_t)64 * band.H * band.W * 4 > kMaxTileSpanBytes ||
@@ -323,8 +328,12 @@ int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     SplitArgs a{};
     a.in = band.in; a.wk = band.wk; a.out = band.out; a.epi = band.epi;
     a.B = band.B; a.H = band.H; a.W = band.W; a.F = band.F;
-    a.nq = band.W / 4 + 2;
-    a.nqo = band.W / 4;
+    // Rows wider than 56 run as column tiles of at most 56 (the ring holds a
+    // tile's columns plus a quad of halo on each side).
+    a.ncol = (band.W + 55) / 56;
+    a.Wt = ((band.W + a.ncol - 1) / a.ncol + 3) & ~3;
+    a.nq = a.Wt / 4 + 2;
+    a.nqo = a.Wt / 4;
     if (2 * 8 * a.nq > 256 || 4 * 8 * a.nq > kNT || 2 * 64 * a.nqo > kStoreItems * 256) return SEERA_OK;
     const int lds = kWPieces * 16 + kNRing * 2 * (4 * a.nq) * 64 + kStageBytes + 16;
     if (lds > kBandMaxLds) return SEERA_OK;
@@ -333,12 +342,12 @@ int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     const int ncu = device_cus();
     double best = 1e30;
     for (int L = 2; L < a.H + 2; L += 2) {
-        const int64_t blocks = (int64_t)a.B * ((a.H + L - 1) / L) * band.nftiles;
+        const int64_t blocks = (int64_t)a.B * ((a.H + L - 1) / L) * a.ncol * band.nftiles;
         const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + 1) / 2 + 1.5);
         if (cost < best) { best = cost; a.L = L; }
     }
     a.nstrip = (a.H + a.L - 1) / a.L;
-    const int64_t nblocks = (int64_t)a.B * a.nstrip;
+    const int64_t nblocks = (int64_t)a.B * a.nstrip * a.ncol;
     if (nblocks > 0x7fffffff || band.nftiles > 65535) return SEERA_OK;
     hipError_t e;
     if (a.epi.act == kActRelu) e = launch<kEpiBiasRelu>(a, (int)nblocks, band.nftiles, lds, st);
