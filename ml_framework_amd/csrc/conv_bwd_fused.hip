@@ -92,7 +92,9 @@ struct FusedArgs {
     int B, H, W;
     int L, nstrip, nsplit;
     int BCY, BCX;       // ring pixels per (row, plane)
-    int QW;             // column quads per row (W / 4)
+    int ncol, Wt;       // column tiles per row, columns per tile (W > 56: tiles of <= 56)
+    int QW;             // X column quads per tile row (Wt / 4)
+    int HQ;             // dY halo quads on each side of a tile (1 with column tiles, else 0)
     int64_t lds_bytes;
 };
 
@@ -111,7 +113,9 @@ template <int NKB>
 __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int split = blockIdx.x;
-    const int b = split / a.nstrip, strip = split - b * a.nstrip;
+    const int ct = split % a.ncol, bs = split / a.ncol;
+    const int b = bs / a.nstrip, strip = bs - b * a.nstrip;
+    const int c0 = ct * a.Wt;                  // first column of the tile
     const int h0 = strip * a.L;
     const int Lb = min(a.L, a.H - h0);         // X / dX rows of this strip
     const int nsteps = (Lb + kG - 1) / kG;
@@ -127,21 +131,27 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     const uint32_t cstride = (uint32_t)(HW * 4);
     const rsrc_t ysrc = make_rsrc(a.dy + (int64_t)b * 64 * HW);
     const rsrc_t xsrc = make_rsrc(a.x + (int64_t)b * 64 * HW);
-    const int row_items = 8 * a.QW;            // items (8 channels x 4 columns) per row
+    // Items (8 channels x 4 columns) per row: X rows hold the tile's QW
+    // quads, dY rows HQ more quads of halo on either side.
+    const int QY = a.QW + 2 * a.HQ;
+    const int row_items_x = 8 * a.QW, row_items_y = 8 * QY;
     const bool db_on = a.dbpart != nullptr;
 
-    // Item `it` of a group of rows: (row rr, plane, 8-channel group cg, column
-    // quad q4), cg fastest. Its 8 loads (one float4 per channel) and its ring
-    // offset for pixel 4*q4 + pad.
-    auto item_load = [&](rsrc_t src, int it, int img_row, bool ok, floatx4 (&v)[8]) {
-        const int cg = it & 3, q4 = (it >> 2) % a.QW, plane = (it >> 2) / a.QW;
-        const uint32_t vo = ok && (unsigned)img_row < (unsigned)a.H
-            ? (uint32_t)((((plane * 32 + cg * 8) * a.H + img_row) * a.W + 4 * q4) * 4) : kBufOOB;
+    // Item `it` of a group of rows (nq quads per row, hq of them halo on the
+    // left): (row rr, plane, 8-channel group cg, column quad q4), cg fastest;
+    // quad q4 holds columns c0 + 4*(q4 - hq) .. + 3 (zeros outside the image).
+    // Its 8 loads (one float4 per channel) and its ring offset for pixel
+    // 4*(q4 - hq) + pad.
+    auto item_load = [&](rsrc_t src, int nq, int hq, int it, int img_row, bool ok, floatx4 (&v)[8]) {
+        const int cg = it & 3, q4 = (it >> 2) % nq, plane = (it >> 2) / nq;
+        const int col = c0 + 4 * (q4 - hq);
+        const uint32_t vo = ok && (unsigned)img_row < (unsigned)a.H && (unsigned)col < (unsigned)a.W
+            ? (uint32_t)((((plane * 32 + cg * 8) * a.H + img_row) * a.W + col) * 4) : kBufOOB;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = buf_load4s(src, vo, j * cstride);
     };
-    auto item_store = [&](half_t* ring_row, int P, int pad, int it, const floatx4 (&v)[8]) {
-        const int cg = it & 3, q4 = (it >> 2) % a.QW, plane = (it >> 2) / a.QW;
+    auto item_store = [&](half_t* ring_row, int P, int pad, int nq, int hq, int it, const floatx4 (&v)[8]) {
+        const int cg = it & 3, q4 = (it >> 2) % nq, plane = (it >> 2) / nq;
         half_t* dst = ring_row + plane * P;
         const int sw = q4 & 1;  // odd quads write their pixel pairs swapped
 #pragma unroll
@@ -149,8 +159,13 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             float col[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) col[j] = sw ? v[j][jj ^ 1] : v[j][jj];
-            *reinterpret_cast<half8*>(dst + ring_off(4 * q4 + pad + (jj ^ sw), cg)) = pack8(col);
+            *reinterpret_cast<half8*>(dst + ring_off(4 * (q4 - hq) + pad + (jj ^ sw), cg)) = pack8(col);
         }
+    };
+    // A dY item's quad is the tile's own (not halo): only those enter db.
+    auto own_y = [&](int it) {
+        const int q4 = ((it % row_items_y) >> 2) % QY;
+        return q4 >= a.HQ && q4 < a.QW + a.HQ;
     };
     // Bias gradient: the producers sum each dY item of the strip's own rows
     // (dY rows h0 .. h0 + Lb - 1) per channel, in fp32 before rounding.
@@ -169,16 +184,17 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     // zeroed ----
     {
         floatx4 pv[2][8];
-        // producers ptid < 2*row_items: dY items it = ptid + 2*row_items*k of
-        // rows 0..3, the channels of their loop item (so one set of bias
-        // sums serves both); consumers tid < 2*row_items: X item tid of rows 0, 1
-        const bool pro = tid < kCons ? tid < 2 * row_items : ptid < 2 * row_items;
+        // producers ptid < 2*row_items_y: dY items it = ptid + 2*row_items_y*k
+        // of rows 0..3, the channels of their loop item (so one set of bias
+        // sums serves both); consumers tid < 2*row_items_x: X item tid of rows 0, 1
+        const bool pro = tid < kCons ? tid < 2 * row_items_x : ptid < 2 * row_items_y;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int it = (producer ? ptid : tid) + k * 2 * row_items;
-            const int rr = it / row_items;
-            if (producer) item_load(ysrc, it % row_items, h0 - 1 + rr, pro && rr <= Lb + 1, pv[k]);
-            else if (k == 0) item_load(xsrc, it % row_items, h0 + rr, pro && rr < Lb, pv[k]);
+            const int ri = producer ? row_items_y : row_items_x;
+            const int it = (producer ? ptid : tid) + k * 2 * ri;
+            const int rr = it / ri;
+            if (producer) item_load(ysrc, QY, a.HQ, it % ri, h0 - 1 + rr, pro && rr <= Lb + 1, pv[k]);
+            else if (k == 0) item_load(xsrc, a.QW, 0, it % ri, h0 + rr, pro && rr < Lb, pv[k]);
         }
         // The flipped weights, per 32-filter chunk: the fp32 rows of its
         // filters (float4 i = k * kNT + tid of the chunk's 18432 floats),
@@ -219,29 +235,33 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             }
         }
         __syncthreads();  // the staging copy is read: the rings may be written
-        // padding pixels: dY ring [0, kYPad) and [W + kYPad, BCY), X ring
-        // [0, kXPad) and [W + kXPad, BCX), of every (row, plane), 4 chunks each
+        // pixels no item writes: dY ring [0, ylo) and [ylo + 4*QY, BCY), X
+        // ring [0, kXPad) and [kXPad + Wt, BCX), of every (row, plane), 4
+        // chunks each (ylo = kYPad - 4*HQ)
         const half8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
-        const int nyp = a.BCY - a.W, nxp = a.BCX - a.W;
+        const int ylo = kYPad - 4 * a.HQ;
+        const int nyp = a.BCY - 4 * QY, nxp = a.BCX - a.Wt;
         const int nzy = kNRY * 2 * nyp * 4, nz = nzy + kNRX * 2 * nxp * 4;
         for (int i = tid; i < nz; i += kNT) {
             const bool y = i < nzy;
-            const int iz = y ? i : i - nzy, np = y ? nyp : nxp, pad = y ? kYPad : kXPad;
+            const int iz = y ? i : i - nzy, np = y ? nyp : nxp;
+            const int lo = y ? ylo : kXPad, span = y ? 4 * QY : a.Wt;
             const int rest = iz >> 2, pp = rest % np, rp = rest / np;
-            const int px = pp < pad ? pp : a.W + pp;
+            const int px = pp < lo ? pp : span + pp;
             *reinterpret_cast<half8*>((y ? ry + rp * PY : rx + rp * PX) + px * 32 + (iz & 3) * 8) = z8;
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int it = (producer ? ptid : tid) + k * 2 * row_items;
-            const int rr = it / row_items;
+            const int ri = producer ? row_items_y : row_items_x;
+            const int it = (producer ? ptid : tid) + k * 2 * ri;
+            const int rr = it / ri;
             if (producer) {
                 if (pro) {
-                    item_store(ry + rr * 2 * PY, PY, kYPad, it % row_items, pv[k]);
-                    if (db_on && rr >= 1 && rr <= Lb) item_sum(pv[k], dsum);
+                    item_store(ry + rr * 2 * PY, PY, kYPad, QY, a.HQ, it % ri, pv[k]);
+                    if (db_on && rr >= 1 && rr <= Lb && own_y(it)) item_sum(pv[k], dsum);
                 }
             } else if (k == 0 && pro) {
-                item_store(rx + rr * 2 * PX, PX, kXPad, it % row_items, pv[k]);
+                item_store(rx + rr * 2 * PX, PX, kXPad, a.QW, 0, it % ri, pv[k]);
             }
         }
     }
@@ -336,14 +356,15 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
                 // lane holds pixels 4*kc + (0..3) of group pg at channel lane % 16
                 const int i = i0 + dr;
                 if (i < Lb) {
-                    const int orow = (h0 + i) * a.W;
+                    const int orow = (h0 + i) * a.W + c0;
 #pragma unroll
                     for (int pg = 0; pg < 2; ++pg) {
                         const int px = 32 * pxh + 16 * pg + 4 * kc;
 #pragma unroll
                         for (int cs = 0; cs < 2; ++cs) {
                             const int c = 16 * (2 * chh + cs) + (lane & 15);
-                            const uint32_t off = px < a.W ? (uint32_t)((c * HW + orow + px) * 4) : kBufOOB;
+                            const uint32_t off = px < a.Wt && c0 + px < a.W
+                                ? (uint32_t)((c * HW + orow + px) * 4) : kBufOOB;
                             __builtin_amdgcn_raw_buffer_store_b128(
                                 __builtin_bit_cast(uintx4_t, ad[pg][cs]), dxdst, off, 0, 0);
                         }
@@ -424,14 +445,19 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
 #pragma unroll
         for (int k = 0; k < kItems; ++k) {
             const int it2 = ptid;
-            const int rr = it2 < 2 * row_items ? it2 / row_items : 2;
-            const int ir = it2 % row_items;
-            const int cg = ir & 3, q4 = (ir >> 2) % a.QW, plane = (ir >> 2) / a.QW;
-            const int pad = pisy[k] ? kYPad : kXPad;
-            rbase[k] = rr < 2 ? (pisy[k] ? h0 + 1 : h0) + rr : INT_MAX / 2;
-            pbase[k] = (((plane * 32 + cg * 8) * a.H) * a.W + 4 * q4) * 4 + (rr < 2 ? rbase[k] * W4 : 0);
+            const int ri = pisy[k] ? row_items_y : row_items_x, nq = pisy[k] ? QY : a.QW;
+            const int hq = pisy[k] ? a.HQ : 0;
+            const int rr = it2 < 2 * ri ? it2 / ri : 2;
+            const int ir = it2 % ri;
+            const int cg = ir & 3, q4 = (ir >> 2) % nq, plane = (ir >> 2) / nq;
+            const int pad = (pisy[k] ? kYPad : kXPad) - 4 * hq;
+            const int col = c0 + 4 * (q4 - hq);
+            const bool cin = (unsigned)col < (unsigned)a.W;  // else: zeros, every step
+            rbase[k] = rr < 2 && cin ? (pisy[k] ? h0 + 1 : h0) + rr : INT_MAX / 2;
+            pbase[k] = (((plane * 32 + cg * 8) * a.H) * a.W + col) * 4 + (rbase[k] < a.H ? rbase[k] * W4 : 0);
+            const bool own = !pisy[k] || (q4 >= hq && q4 < a.QW + hq);
             pmeta[k] = (plane * (pisy[k] ? PY : PX) + (4 * q4 + pad) * 32) | (cg << 24) |
-                       (((2 * q4 + pad / 2) & 3) << 26) | (rr << 28);
+                       (((2 * q4 + pad / 2) & 3) << 26) | (rr << 28) | (own ? 1 << 30 : 0);
         }
         auto load_item = [&](int sn, int k, floatx4 (&v)[8]) {
             const bool ok = rbase[k] + 2 * sn < rlim[k];
@@ -444,7 +470,7 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
                 // dY strip row j = 2sn + 2 + rr up to the last step's window
                 // (rows past Lb + 1 are zeros), X strip rows up to 2*nsteps
                 // (rows past the strip are zeros)
-                const int prr = pmeta[k] >> 28, pcg = (pmeta[k] >> 24) & 3, prq = (pmeta[k] >> 26) & 3;
+                const int prr = (pmeta[k] >> 28) & 3, pcg = (pmeta[k] >> 24) & 3, prq = (pmeta[k] >> 26) & 3;
                 const int r = 2 * sn + prr + (pisy[k] ? 2 : 0);
                 if (prr < 2 && r < 2 * nsteps + (pisy[k] ? 2 : 0)) {
                     half_t* dst = (pisy[k] ? ry + (r % kNRY) * 2 * PY : rx + (r % kNRX) * 2 * PX) +
@@ -459,7 +485,7 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
                         *reinterpret_cast<half8*>(dst + q * 32 + ((pcg ^ ((prq + (q >> 1)) & 3)) << 3)) =
                             pack8(col);
                     }
-                    if (db_on && pisy[k] && r <= Lb) item_sum(v, dsum);
+                    if (db_on && pisy[k] && r <= Lb && ((pmeta[k] >> 30) & 1)) item_sum(v, dsum);
                 }
             }
         };
@@ -488,15 +514,15 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     }
     if (db_on) {
         // The producers' sums meet in LDS once every consumer is past its
-        // last ring read: thread ptid < 2*row_items holds the sums of in-row
-        // item ptid % row_items over its rows (rr = ptid / row_items, + 2
+        // last ring read: thread ptid < 2*row_items_y holds the sums of in-row
+        // item ptid % row_items_y over its rows (rr = ptid / row_items_y, + 2
         // per step, and the prologue's rows 1..3).
         __syncthreads();
         // (the producer index is rebuilt from the wave and lane ids rather
         // than kept live through the loop, where every register is taken)
         const int ptid = wave * 64 + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) - kCons;
         floatx4* const red = reinterpret_cast<floatx4*>(smem);
-        if (producer && ptid < 2 * row_items) {
+        if (producer && ptid < 2 * row_items_y) {
             red[2 * ptid] = floatx4{dsum[0], dsum[1], dsum[2], dsum[3]};
             red[2 * ptid + 1] = floatx4{dsum[4], dsum[5], dsum[6], dsum[7]};
         }
@@ -507,8 +533,8 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             const float* redf = reinterpret_cast<const float*>(smem);
             float sum = 0.f;
             for (int rr = 0; rr < 2; ++rr)
-                for (int q4 = 0; q4 < a.QW; ++q4) {
-                    const int slot = rr * row_items + (plane * a.QW + q4) * 4 + cg;
+                for (int q4 = 0; q4 < QY; ++q4) {
+                    const int slot = rr * row_items_y + (plane * QY + q4) * 4 + cg;
                     sum += redf[slot * 8 + j];
                 }
             a.dbpart[(int64_t)split * 64 + f] = sum;
@@ -524,7 +550,7 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     *used = false;
     if (C != 64 || F != 64 || R != 3 || S != 3 || sh != 1 || sw != 1 || ph != 1 || pw != 1)
         return SEERA_OK;
-    if (B < 1 || H < 1 || W < 4 || W % 4 != 0 || W > 56) return SEERA_OK;
+    if (B < 1 || H < 1 || W < 4 || W % 4 != 0) return SEERA_OK;
     if (((reinterpret_cast<uintptr_t>(dY) | reinterpret_cast<uintptr_t>(X) |
           reinterpret_cast<uintptr_t>(dX) | reinterpret_cast<uintptr_t>(Wconv)) & 15) != 0)
         return SEERA_OK;
@@ -532,29 +558,40 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     FusedArgs a{};
     a.dy = dY; a.x = X; a.dx = dX; a.w = Wconv;
     a.B = B; a.H = H; a.W = W;
-    a.QW = W / 4;
+    // Rows wider than 56 run as column tiles of at most 56: each tile's dY
+    // rows carry one quad of halo on either side (the dX of its edge columns
+    // reads one dY column past them; dW pairs the tile's own X columns with
+    // them), and db counts only the tile's own dY columns.
+    a.ncol = (W + 55) / 56;
+    a.Wt = ((W + a.ncol - 1) / a.ncol + 3) & ~3;
+    a.HQ = a.ncol > 1 ? 1 : 0;
+    a.QW = a.Wt / 4;
+    const int QY = a.QW + 2 * a.HQ;
+    if (2 * 8 * QY > kProd || 2 * 8 * a.QW > kCons) return SEERA_OK;  // items per row pair
     // K blocks of 32 dY pixels cover ring pixels [0, 32*nkb), i.e. columns
-    // [-4, 32*nkb - 4); the dX fragments reach ring pixel W + 4.
-    const int nkb = (W + 5 + 31) / 32;
+    // [-4, 32*nkb - 4) of the tile; the dX fragments reach ring pixel Wt + 4.
+    const int nkb = (a.Wt + 5 + 31) / 32;
     a.BCY = 32 * nkb;
     a.BCX = 32 * nkb + kXPad;
+    if (a.BCY < kYPad - 4 * a.HQ + 4 * QY) return SEERA_OK;  // the halo quad must fit the ring
     a.lds_bytes = (int64_t)kWHalves * 2 + (int64_t)kNRY * 2 * a.BCY * 64 + (int64_t)kNRX * 2 * a.BCX * 64;
     if (a.lds_bytes > kBandMaxLds) return SEERA_OK;
     // the db reduction reuses the rings: 2 rows of items x 8 floats; the
     // weight build stages one chunk (18432 halves) there
-    if ((int64_t)2 * 8 * a.QW * 32 > a.lds_bytes) return SEERA_OK;
+    if ((int64_t)2 * 8 * QY * 32 > a.lds_bytes) return SEERA_OK;
     if ((int64_t)kNRY * 2 * a.BCY * 32 + (int64_t)kNRX * 2 * a.BCX * 32 < 32 * 576) return SEERA_OK;
     // Strip length: fewest rounds of one block per CU, each about (steps + 2)
     // step times.
     const int ncu = device_cus();
     double best = 1e30;
     for (int L = kG; L < H + kG; L += kG) {
-        const int64_t blocks = (int64_t)B * ((H + L - 1) / L);
+        const int64_t blocks = (int64_t)B * ((H + L - 1) / L) * a.ncol;
         const double cost = (double)((blocks + ncu - 1) / ncu) * ((L + kG - 1) / kG + 2);
         if (cost < best) { best = cost; a.L = L; }
     }
     a.nstrip = (H + a.L - 1) / a.L;
-    a.nsplit = B * a.nstrip;
+    if ((int64_t)B * a.nstrip * a.ncol > 0x7fffffff) return SEERA_OK;
+    a.nsplit = B * a.nstrip * a.ncol;
     const size_t part_n = (size_t)a.nsplit * 64 * 576, db_n = db ? (size_t)a.nsplit * 64 : 0;
     void* ws = nullptr;
     SEERA_TRY(workspace(sizeof(float) * (part_n + db_n), &ws, st));

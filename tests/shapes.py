@@ -128,6 +128,9 @@ CONV2D_FUSED = [
     ("f04", 2, 64, 20, 52, 64, 3, 3, 1, 1),
     ("f05", 1, 64, 40, 24, 64, 3, 3, 1, 1),
     ("f06", 4, 64, 57, 56, 64, 3, 3, 1, 1),
+    # rows wider than 56: column tiles with one quad of dY halo on either side
+    ("f07", 1, 64, 7, 200, 64, 3, 3, 1, 1),    # 4 tiles of 52 (the last 44)
+    ("f08", 2, 64, 9, 112, 64, 3, 3, 1, 1),    # 2 tiles of 56
 ]
 
 # Testing/test_1.py:398-470 -- (name, N, Cin, H, W, Cout, KH, KW, stride, pad)

@@ -149,6 +149,7 @@ BWD_BIAS = [
     ("stream_wide", 2, 32, 9, 136, 40, 3, 1, 1),          # dW + db in 3 column tiles
     ("stream_many", 130, 32, 6, 8, 256, 3, 1, 1),         # strips across image boundaries
     ("s2d_stem", 2, 3, 20, 24, 8, 7, 2, 3),               # 7x7 s2 in space-to-depth form
+    ("fused_tiles", 2, 64, 9, 116, 64, 3, 1, 1),          # one-pass dX + dW + db, 3 column tiles
 ]
 
 
