@@ -257,18 +257,10 @@ __global__ __launch_bounds__(256) void widen_rows(const float* __restrict__ in,
 }
 
 // A staging buffer for a re-laid-out operand; *got is false (and nothing is
-// reported) when the device is out of memory for it, so that the caller takes
-// the path that needs no copy.
+// reported) when it cannot be had (out of memory, or a grow under graph
+// capture), so that the caller takes the path that needs no copy.
 int stage(size_t bytes, void** out, hipStream_t st, bool* got) {
-    *got = false;
-    const int e = staging_workspace(bytes, out, st);
-    if (e == SEERA_ERR_OUT_OF_MEMORY) {
-        clear_error();
-        return SEERA_OK;
-    }
-    SEERA_TRY(e);
-    *got = true;
-    return SEERA_OK;
+    return staging_workspace_try(bytes, out, st, got);
 }
 
 // Copies `n` tensors of rows[i] rows x W[i] floats into one staging buffer,

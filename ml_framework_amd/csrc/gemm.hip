@@ -207,6 +207,34 @@ __global__ void fill_zero_2d(float* __restrict__ C, int M, int N, int64_t ldc) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// out [rows_out, ld_out] = in [rows_in, cols_in] (leading dimension ld_in),
+// zero past its rows and columns; ld_out % 4 == 0 (one float4 store per thread).
+__global__ __launch_bounds__(256) void pad_2d(const float* __restrict__ in, int64_t ld_in,
+                                              int rows_in, int cols_in, float* __restrict__ out,
+                                              int rows_out, int ld_out) {
+    const int nq = ld_out / 4;
+    const int64_t n = (int64_t)rows_out * nq;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / nq;
+        const int c0 = (int)(i - r * nq) * 4;
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (r < rows_in) {
+            const float* src = in + r * ld_in;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (c0 + j < cols_in) v[j] = src[c0 + j];
+        }
+        *reinterpret_cast<floatx4*>(out + r * ld_out + c0) = v;
+    }
+}
+
+// GEMMs of at least this many multiply-adds whose operands are not
+// vector-aligned (or whose K is not a whole number of 32-deep slices) run on
+// zero-padded copies of both operands: two copy passes cost less than the
+// scalar loads (4095^3: 1.8 ms on scalar loads) or the non-streaming kernel.
+constexpr double kPadMinMacs = 4294967296.0;
+
 // Dispatch on operand vector-load eligibility. Only the 64x64 tile carries the
 // scalar (any shape / alignment) variants.
 // Optional fused forward epilogue of gemm_dispatch<..., true>.
@@ -219,7 +247,7 @@ struct Epi {
 template <bool A_KC, bool B_KC, bool EPI = false, bool COLSUM = false>
 int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                   int64_t ldc, int M, int N, int K, hipStream_t st, Epi epi = Epi{},
-                  float* colsum = nullptr) {
+                  float* colsum = nullptr, bool padded = false) {
     if (M == 0 || N == 0) return SEERA_OK;
     if (K == 0) {
         // Empty contraction: C = 0 (the reference's K loop never runs), then
@@ -248,8 +276,41 @@ int gemm_dispatch(const float* A, int64_t lda, const float* B, int64_t ldb, floa
         return fail(SEERA_ERR_INVALID_ARGUMENT,
                     "GEMM leading dimension too large for 32-bit tile offsets (lda=%lld ldb=%lld)",
                     (long long)lda, (long long)ldb);
-    const bool va = aligned16(A) && lda % 4 == 0 && (A_KC ? K : M) % 4 == 0;
-    const bool vb = aligned16(B) && ldb % 4 == 0 && (B_KC ? K : N) % 4 == 0;
+    // (padded: the staging copies below, whose rows run on in zeros or in
+    // rows that are never stored up to a multiple of 4, so that every float4
+    // load stays inside the copy)
+    const bool va = padded || (aligned16(A) && lda % 4 == 0 && (A_KC ? K : M) % 4 == 0);
+    const bool vb = padded || (aligned16(B) && ldb % 4 == 0 && (B_KC ? K : N) % 4 == 0);
+    if (!padded && (!va || !vb || K % 32 != 0) && (double)M * N * K >= kPadMinMacs) {
+        // Both operands into a staging copy: K-contiguous [rows][K32], or
+        // MN-contiguous [K32][rows rounded up to 4], zeros past the data.
+        // The zero k slices add nothing (and nothing to the column sums).
+        const int K32 = (K + 31) & ~31, M4 = (M + 3) & ~3, N4 = (N + 3) & ~3;
+        const int64_t na = A_KC ? (int64_t)M * K32 : (int64_t)K32 * M4;
+        const int64_t nb = B_KC ? (int64_t)N * K32 : (int64_t)K32 * N4;
+        const int64_t na_al = (na + 63) & ~(int64_t)63;
+        void* ws = nullptr;
+        bool got = false;
+        SEERA_TRY(staging_workspace_try(sizeof(float) * (size_t)(na_al + nb), &ws, st, &got));
+        if (got) {
+            float* Ap = static_cast<float*>(ws);
+            float* Bp = Ap + na_al;
+            auto pad = [&](const float* in, int64_t ld_in, int rows_in, int cols_in, float* out,
+                           int rows_out, int ld_out) {
+                const int64_t q = (int64_t)rows_out * (ld_out / 4);
+                const unsigned blocks = (unsigned)std::min<int64_t>((q + 255) / 256, 8192);
+                hipLaunchKernelGGL(pad_2d, dim3(blocks), dim3(256), 0, st, in, ld_in, rows_in, cols_in,
+                                   out, rows_out, ld_out);
+            };
+            if (A_KC) pad(A, lda, M, K, Ap, M, K32);
+            else pad(A, lda, K, M, Ap, K32, M4);
+            if (B_KC) pad(B, ldb, N, K, Bp, N, K32);
+            else pad(B, ldb, K, N, Bp, K32, N4);
+            SEERA_HIP_TRY(hipGetLastError());
+            return gemm_dispatch<A_KC, B_KC, EPI, COLSUM>(Ap, A_KC ? K32 : M4, Bp, B_KC ? K32 : N4, C,
+                                                          ldc, M, N, K32, st, epi, colsum, true);
+        }
+    }
     const Plan pl = plan_tiles(M, N, K, va && vb && big_ok, true, true);
     auto fill = [&](auto prob) {
         prob.A = A; prob.B = B; prob.C = C;

@@ -132,6 +132,30 @@ int staging_workspace(size_t bytes, void** out, hipStream_t st) {
     return pool_get(g_stage_pool, bytes, out, st);
 }
 
+int staging_workspace_try(size_t bytes, void** out, hipStream_t st, bool* got) {
+    *out = nullptr;
+    *got = false;
+    if (g_fixed_owner) return SEERA_OK;
+    int dev = 0;
+    SEERA_HIP_TRY(hipGetDevice(&dev));
+    const bool cap = stream_capturing(st);
+    int e;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        e = g_stage_pool.get(dev, st, bytes, cap, out);
+    }
+    if (e == WorkspacePool<HipBackend>::kGrowUnderCapture) return SEERA_OK;
+    if (e == SEERA_ERR_OUT_OF_MEMORY) {
+        (void)hipGetLastError();  // the failed hipMalloc's status, so later launch checks do not see it
+        clear_error();
+        *out = nullptr;
+        return SEERA_OK;
+    }
+    if (e != SEERA_OK) return e;
+    *got = true;
+    return SEERA_OK;
+}
+
 int workspace(size_t bytes, void** out, hipStream_t st) {
     *out = nullptr;
     if (g_fixed_owner) {

@@ -39,6 +39,11 @@ int workspace(size_t bytes, void** out, hipStream_t st);
 // staged in a new layout before a call that itself takes workspace() (the two
 // never alias). Not available under FixedWorkspace.
 int staging_workspace(size_t bytes, void** out, hipStream_t st);
+// The same, for a staging copy the caller can do without: where the buffer
+// cannot be had without allocating under graph capture or a fixed workspace,
+// or the device is out of memory for it, returns SEERA_OK with *got false and
+// nothing reported, so the caller takes its path without the copy.
+int staging_workspace_try(size_t bytes, void** out, hipStream_t st, bool* got);
 
 // Compute units of the current device (256 if the query fails).
 int device_cus();

@@ -34,6 +34,7 @@ SHAPES = [
     (33, 65, 17, 2),       # odd dims, folded batch
     (7, 0, 5, 1),          # K = 0: C = act(bias)
     (4096, 4096, 512, 1),  # 256x256 warp-specialised tiles
+    (2049, 2047, 1025, 1),  # unaligned and large: zero-padded staging copies of A and B
 ]
 
 
@@ -108,6 +109,7 @@ BWD_SHAPES = [
     (64, 64, 4096, 1),     # long contraction over N: split-K, mask in the reduce
     (33, 65, 17, 2),       # odd dims, folded batch
     (2048, 2048, 2048, 1),  # 256x256 warp-specialised tiles
+    (2049, 2047, 1025, 1),  # unaligned and large: zero-padded staging copies
     (5, 0, 7, 1),          # K = 0: empty dA and dB
 ]
 

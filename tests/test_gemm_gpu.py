@@ -150,6 +150,38 @@ def test_matmul_bwd_parity(M, K, N, nb):
     assert rel_fro(da, rda) <= STRICT and rel_fro(db, rdb) <= STRICT
 
 
+# Large GEMMs whose operands are not vector-aligned, or whose K is not a
+# whole number of 32-deep slices, run on zero-padded staging copies of both
+# operands (odd everything; aligned with K % 32 != 0; a folded batch).
+PADDED = [(2049, 2047, 1025, 1), (1024, 4100, 1024, 1), (700, 2051, 1001, 3)]
+
+
+@pytest.mark.parametrize("M,K,N,nb", PADDED)
+def test_padded_large_gemm_parity(M, K, N, nb):
+    r = np.random.default_rng(M + 3 * K + 7 * N + nb)
+    a = r.uniform(-1, 1, (nb, M, K)).astype(np.float32)
+    b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    dc = r.uniform(-1, 1, (nb, M, N)).astype(np.float32)
+    got = hip_matmul(a, b)
+    ref = S.matmul_batched(fp16r(a), fp16r(b))
+    assert_parity(got, ref, f"fwd {M}x{K}x{N}x{nb}")
+    assert rel_fro(got, ref) <= STRICT
+    da, db = hip_matmul_bwd(a, b, dc)
+    rda, rdb = S.matmul_bwd(fp16r(a), fp16r(b), fp16r(dc))
+    assert_parity(da, rda, "dA")
+    assert_parity(db, rdb, "dB")
+    assert rel_fro(da, rda) <= STRICT and rel_fro(db, rdb) <= STRICT
+
+
+def test_padded_gemm_identity_bit_exact():
+    """The zero-padded copies add only zero products: A @ I and I @ A return
+    fp16r(A) bit for bit on a 2049 x 2047 operand."""
+    r = np.random.default_rng(2049)
+    a = r.uniform(-8, 8, (2049, 2047)).astype(np.float32)
+    assert np.array_equal(hip_matmul(a, np.eye(2047, dtype=np.float32)), fp16r(a))
+    assert np.array_equal(hip_matmul(np.eye(2049, dtype=np.float32), a), fp16r(a))
+
+
 def test_matmul_2d_and_3d_entry_agree():
     """cuTen passes Nbatch=1 for 2-D A (cuTen.py:423-445)."""
     r = np.random.default_rng(5)
