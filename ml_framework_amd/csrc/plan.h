@@ -91,6 +91,24 @@ inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split,
 // Deterministic split-K reduction: C[m, n] = sum_z P[z][m][n] in z order;
 // blocks from nb_c on add the column sums of a kColSum problem instead,
 // out[n] = sum_z cs[z*N + n] (same launch).
+// sum_z P[z * stride + i] in z order, 16 loads in flight (a loop of single
+// loads waits a memory round trip per split: 58 us for 256 splits of 64x64).
+__device__ __forceinline__ float split_sum(const float* __restrict__ P, int64_t stride, int splits,
+                                           int64_t i) {
+    constexpr int kU = 16;
+    float s = 0.f;
+    int z = 0;
+    for (; z + kU <= splits; z += kU) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = P[(z + u) * stride + i];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) s += v[u];
+    }
+    for (; z < splits; ++z) s += P[z * stride + i];
+    return s;
+}
+
 static __global__ void splitk_reduce(const float* __restrict__ P, float* __restrict__ C,
                                      int M, int N, int64_t ldc, int splits, int64_t stride,
                                      int nb_c, const float* __restrict__ cs,
@@ -98,16 +116,12 @@ static __global__ void splitk_reduce(const float* __restrict__ P, float* __restr
     if ((int)blockIdx.x >= nb_c) {
         const int n = ((int)blockIdx.x - nb_c) * blockDim.x + threadIdx.x;
         if (n >= N) return;
-        float s = 0.f;
-        for (int z = 0; z < splits; ++z) s += cs[(int64_t)z * N + n];
-        cs_out[n] = s;
+        cs_out[n] = split_sum(cs, N, splits, n);
         return;
     }
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * N) return;
-    float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += P[z * stride + i];
-    C[(i / N) * ldc + i % N] = s;
+    C[(i / N) * ldc + i % N] = split_sum(P, stride, splits, i);
 }
 
 // Problems that declare `static constexpr bool kWsStream = true` supply
@@ -124,8 +138,7 @@ static __global__ void splitk_reduce_epi(const float* __restrict__ P, float* __r
                                          int act) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * N) return;
-    float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += P[z * stride + i];
+    const float s = split_sum(P, stride, splits, i);
     const int n = (int)(i % N);
     const int64_t o = (i / N) * ldc + n;
     epilogue(C + o, mask ? mask + o : nullptr, s, bias ? bias[n] : 0.f, act);
