@@ -559,6 +559,39 @@ def bench_conv_layers(steps, warmup, stream):
     return out
 
 
+# GEMM shapes beyond config 2 (Nbatch, M, K, N): odd extents (the staging
+# copies), K not a whole number of 32-deep slices, folded batches, tall and
+# skinny shapes (split-K).
+GEMM_SHAPES = [
+    (1, 4095, 4095, 4095), (1, 4097, 4097, 4097), (1, 4096, 4095, 4096), (1, 3000, 3000, 3000),
+    (1, 1000, 1000, 1000), (16, 512, 512, 512), (8, 1024, 1024, 1024), (1, 8192, 1024, 8192),
+    (1, 64, 65536, 64), (1, 65536, 64, 64),
+]
+
+
+def bench_gemm_shapes(steps, warmup, stream):
+    """Forward and backward (dA + dB) time of each GEMM_SHAPES entry:
+    {"NbxMxKxN": [ms_fwd, ms_bwd], ...}."""
+    r = np.random.default_rng(5)
+    lib = capi.load()
+    out = {}
+    for (nb, M, K, N) in GEMM_SHAPES:
+        a = r.uniform(-1, 1, (nb, M, K)).astype(np.float32)
+        b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+        dc = r.uniform(-1, 1, (nb, M, N)).astype(np.float32)
+        bufs = [DeviceBuffer.from_array(v) for v in (a, b, dc)]
+        bufs += [DeviceBuffer(dc.nbytes), DeviceBuffer(a.nbytes), DeviceBuffer(b.nbytes)]
+        pa, pb, pdc, pc, pda, pdb = (x.ptr for x in bufs)
+        fwd = lambda: capi.check(lib.seera_hip_matmul_async(pa, pb, pc, M, N, K, nb, stream.ptr))  # noqa: E731
+        bwd = lambda: capi.check(lib.seera_hip_matmul_bwd_async(  # noqa: E731
+            pa, pb, pdc, pda, pdb, M, N, K, nb, stream.ptr))
+        out[f"{nb}x{M}x{K}x{N}"] = [round(timed(fwd, steps, warmup, stream), 4),
+                                    round(timed(bwd, steps, warmup, stream), 4)]
+        for x in bufs:
+            x.close()
+    return out
+
+
 def bench_library_fp16_gemm(steps, warmup, stream, n=4096):
     """The vendor library's fp16-operand GEMM (torch.matmul -> hipBLASLt, fp16
     in and out) at n^3, timed the same way: a yardstick for the clock and MFMA
@@ -591,6 +624,7 @@ WORKLOADS = {
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,
     "conv_layers": bench_conv_layers,
+    "gemm_shapes": bench_gemm_shapes,
     "library_fp16_gemm4096": bench_library_fp16_gemm,
     "convT_cfg5": bench_convT,
     "maxpool_2x2_s2": lambda steps, warmup, st: bench_maxpool(steps, warmup, st, 2, 2, 0),
