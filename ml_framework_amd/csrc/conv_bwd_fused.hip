@@ -96,6 +96,7 @@ struct FusedArgs {
     int QW;             // X column quads per tile row (Wt / 4)
     int HQ;             // dY halo quads on each side of a tile (1 with column tiles, else 0)
     int64_t lds_bytes;
+    int wbuild_once;    // the rings hold both weight chunks' fp16 copies at once
 };
 
 // The flipped weights in LDS: wl[(chunk * 9 + t*3 + u) * 2048 + w_off(c, k / 8)
@@ -197,41 +198,50 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
             else if (k == 0) item_load(xsrc, a.QW, 0, it % ri, h0 + rr, pro && rr < Lb, pv[k]);
         }
         // The flipped weights, per 32-filter chunk: the fp32 rows of its
-        // filters (float4 i = k * kNT + tid of the chunk's 18432 floats),
-        // their natural-order fp16 copy (filter fl of the chunk, channel c,
-        // tap r*3 + s at half fl*576 + c*9 + r*3 + s), then piece (tap, k
-        // quad kq, c), c fastest, gathers its 8 filters (a 32-lane half reads
-        // 32 distinct banks: 18-byte pixel stride) and writes them as one
-        // 16-byte chunk (8 consecutive c on 8 distinct slots). The second
-        // chunk's loads fly during the first chunk's gathers.
-        floatx4 wf[kWLoads / 2];
-        auto wload = [&](int ch) {
+        // filters (float4 i = k * kNT + tid of the chunk's 18432 floats; both
+        // chunks requested at once), their natural-order fp16 copy (filter fl
+        // of the chunk, channel c, tap r*3 + s at half fl*576 + c*9 + r*3 +
+        // s), then piece (tap, k quad kq, c), c fastest, gathers its 8
+        // filters (a 32-lane half reads 32 distinct banks: 18-byte pixel
+        // stride) and writes them as one 16-byte chunk (8 consecutive c on 8
+        // distinct slots). When the rings hold both chunks' copies, one
+        // barrier serves both; otherwise the chunks take turns.
+        floatx4 wf[kWLoads];
 #pragma unroll
-            for (int k = 0; k < kWLoads / 2; ++k)
-                wf[k] = *reinterpret_cast<const floatx4*>(a.w + ch * 32 * 576 + 4 * (k * kNT + tid));
-        };
+        for (int k = 0; k < kWLoads; ++k) wf[k] = *reinterpret_cast<const floatx4*>(a.w + 4 * (k * kNT + tid));
         half_t* const stg = ry;
-        wload(0);
-        for (int ch = 0; ch < 2; ++ch) {
-            if (ch) __syncthreads();  // chunk 0's pieces are read
+        auto put = [&](int k, half_t* base) {
+            half4 h;
 #pragma unroll
-            for (int k = 0; k < kWLoads / 2; ++k) {
-                half4 h;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) h[q] = to_half(wf[k][q]);
-                *reinterpret_cast<half4*>(stg + 4 * (k * kNT + tid)) = h;
-            }
-            __syncthreads();
-            if (ch == 0) wload(1);
+            for (int q = 0; q < 4; ++q) h[q] = to_half(wf[k][q]);
+            *reinterpret_cast<half4*>(base + 4 * ((k % (kWLoads / 2)) * kNT + tid)) = h;
+        };
+        auto gather = [&](int ch, const half_t* base) {
 #pragma unroll
             for (int m = 0; m < kPieces; ++m) {
                 const int pc = m * kNT + tid;
                 const int c = pc & 63, kq = (pc >> 6) & 3, tap = pc >> 8;
-                const half_t* src = stg + 8 * kq * 576 + c * 9 + (kTaps - 1 - tap);
+                const half_t* src = base + 8 * kq * 576 + c * 9 + (kTaps - 1 - tap);
                 half8 h;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) h[j] = src[j * 576];
                 *reinterpret_cast<half8*>(wl + (ch * kTaps + tap) * 2048 + w_off(c, kq)) = h;
+            }
+        };
+        if (a.wbuild_once) {
+#pragma unroll
+            for (int k = 0; k < kWLoads; ++k) put(k, stg + (k / (kWLoads / 2)) * 32 * 576);
+            __syncthreads();
+            gather(0, stg);
+            gather(1, stg + 32 * 576);
+        } else {
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                if (ch) __syncthreads();  // chunk 0's pieces are read
+#pragma unroll
+                for (int k = 0; k < kWLoads / 2; ++k) put(ch * (kWLoads / 2) + k, stg);
+                __syncthreads();
+                gather(ch, stg);
             }
         }
         __syncthreads();  // the staging copy is read: the rings may be written
@@ -579,7 +589,9 @@ int fused_conv_bwd(const float* dY, const float* Wconv, const float* X, float* d
     // the db reduction reuses the rings: 2 rows of items x 8 floats; the
     // weight build stages one chunk (18432 halves) there
     if ((int64_t)2 * 8 * QY * 32 > a.lds_bytes) return SEERA_OK;
-    if ((int64_t)kNRY * 2 * a.BCY * 32 + (int64_t)kNRX * 2 * a.BCX * 32 < 32 * 576) return SEERA_OK;
+    const int64_t ring_halves = (int64_t)kNRY * 2 * a.BCY * 32 + (int64_t)kNRX * 2 * a.BCX * 32;
+    if (ring_halves < 32 * 576) return SEERA_OK;
+    a.wbuild_once = ring_halves >= 64 * 576;
     // Strip length: fewest rounds of one block per CU, each about (steps + 2)
     // step times.
     const int ncu = device_cus();
