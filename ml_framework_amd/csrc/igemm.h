@@ -213,7 +213,8 @@ struct PipeCfg {
     static constexpr int NTG = Tile::NT;          // threads per group
     static constexpr int NT = NTG * KG;
     static constexpr int STAGE = (BM + BN) * BK;  // halves per LDS stage
-    static constexpr int RED_BYTES = KG > 1 ? NTG * Tile::TM * Tile::TN * 16 * 4 : 0;
+    // groups 1 .. KG-1 hand over their accumulators at once, one slot each
+    static constexpr int RED_BYTES = KG > 1 ? (KG - 1) * NTG * Tile::TM * Tile::TN * 16 * 4 : 0;
     static constexpr int LDS_BYTES =
         KG * Tile::LDS_BYTES > RED_BYTES ? KG * Tile::LDS_BYTES : RED_BYTES;
     static_assert(LDS_BYTES <= 160 * 1024, "LDS tile exceeds the 160 KB of a gfx950 CU");
@@ -318,31 +319,31 @@ __device__ __forceinline__ void pipe_body(const P& p, int bid, int nblk, int z_s
         }
     }
     if constexpr (KG > 1) {
-        // groups 1.. hand their accumulators to group 0, one group at a time
-        // (the stage reads of the last iteration ended at its barrier)
+        // groups 1.. write their accumulators into slots g-1 at once (the
+        // stage reads of the last iteration ended at its barrier); group 0
+        // adds them in group order
         float* const red = reinterpret_cast<float*>(smem_all);
-#pragma unroll 1
-        for (int g = 1; g < KG; ++g) {
-            if (grp == g) {
+        constexpr int kSlot = TM * TN * 16 * NT;
+        if (grp != 0) {
+            float* const mine = red + (grp - 1) * kSlot;
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) red[((i * TN + j) * 16 + r) * NT + tid] = acc[i][j][r];
-            }
-            __syncthreads();
-            if (grp == 0) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * TN + j) * 16 + r) * NT + tid];
-            }
-            __syncthreads();
+                    for (int r = 0; r < 16; ++r) mine[((i * TN + j) * 16 + r) * NT + tid] = acc[i][j][r];
         }
+        __syncthreads();
         if (grp != 0) return;
+#pragma unroll
+        for (int g = 1; g < KG; ++g)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[i][j][r] += red[(g - 1) * kSlot + ((i * TN + j) * 16 + r) * NT + tid];
     }
 
     const int z = z_split;
