@@ -358,13 +358,11 @@ int gemm_pair(const GemmArgs& g1, Epi e1, const GemmArgs& g2, float* colsum2, hi
     if (shapes_ok && !pairable) {
         // An edge that is not a multiple of 4 (the N = 10 head of an MLP):
         // both GEMMs on scalar loads in one launch, when both plans are
-        // unsplit 64x64 tiles within one round of the CUs (a launch costs
+        // unsplit 32x32 or 64x64 tiles within one round of the CUs (a launch costs
         // ~4.5 us at these sizes, more than the scalar loads of a small
         // GEMM); otherwise each on its own best path below.
-        const Plan pl1 = plan_tiles(g1.M, g1.N, g1.K, true, true, true);
-        const Plan pl2 = plan_tiles(g2.M, g2.N, g2.K, true, true, true);
-        if (pl1.tile == Tile::S && pl2.tile == Tile::S && pl1.splits == 1 && pl2.splits == 1 &&
-            tile_count(Tile::S, g1.M, g1.N) + tile_count(Tile::S, g2.M, g2.N) <= kNumCUs) {
+        Plan pl1, pl2;
+        if (pair_plans(g1.M, g1.N, g1.K, g2.M, g2.N, g2.K, pl1, pl2)) {
             GemmProblem<A1_KC, 1, B1_KC, 1, EPI1> p1{};
             p1.A = g1.A; p1.B = g1.B; p1.C = g1.C;
             p1.M = g1.M; p1.N = g1.N; p1.K = g1.K;
@@ -398,8 +396,8 @@ int gemm_pair(const GemmArgs& g1, Epi e1, const GemmArgs& g2, float* colsum2, hi
         p2.M = g2.M; p2.N = g2.N; p2.K = g2.K;
         p2.lda = g2.lda; p2.ldb = g2.ldb; p2.ldc = g2.ldc;
         p2.colsum = colsum2;
-        const Plan pl1 = plan_tiles(g1.M, g1.N, g1.K, true, true, true);
-        const Plan pl2 = plan_tiles(g2.M, g2.N, g2.K, true, true, true);
+        Plan pl1, pl2;
+        pair_plans(g1.M, g1.N, g1.K, g2.M, g2.N, g2.K, pl1, pl2);
         return run_plan_pair<true, true>(p1, pl1, p2, pl2, st);
     }
     SEERA_TRY((gemm_dispatch<A1_KC, B1_KC, EPI1>(g1.A, g1.lda, g1.B, g1.ldb, g1.C, g1.ldc, g1.M,

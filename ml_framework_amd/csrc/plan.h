@@ -16,13 +16,15 @@ namespace seera {
 //   M   128x128x32, 2x2 waves of 64x64 (warp-specialised, 2 producer waves,
 //       when the operands take streaming stagers)
 //   S   64x64x32,   2x2 waves of 32x32  small / odd shapes, scalar loads
-enum class Tile { L, W, M, S };
+//   T   32x32x32,   one wave per K group  GEMMs whose 32x32 tiles fit one round
+//       of the CUs (half the operand bytes per CU of a 64x64 tile)
+enum class Tile { L, W, M, S, T };
 
 struct Plan {
     Tile tile;
     int splits;
     int k_split;
-    int groups = 1;  // wave groups over the K range of a 64x64 block (1, 2 or 4)
+    int groups = 1;  // wave groups over the K range of a 64x64 (1, 2, 4) or 32x32 (1 .. 8) block
 };
 
 constexpr int kNumCUs = 256;
@@ -39,8 +41,15 @@ constexpr int kGroupSplitK = 1024;
 // 67.6 -> 58.5 us; replacing up to 8 splits: 59.3 us.
 constexpr int kMaxGroupSplits = 4;
 
-inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : 64; }
-inline int tile_bn(Tile t) { return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : 64; }
+inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : t == Tile::T ? 32 : 64; }
+inline int tile_bn(Tile t) {
+    return t == Tile::L || t == Tile::W ? 256 : t == Tile::M ? 128 : t == Tile::T ? 32 : 64;
+}
+
+// The cost of a split-K reduce launch in operand floats per CU (the bytes a
+// CU streams in the time of a dependent small launch, about 4.5 us), against
+// which a 32x32 plan's unsplit K range is weighed.
+constexpr double kSplitReduceFloats = 100000.0;
 
 inline int64_t tile_count(Tile t, int M, int N) {
     return (int64_t)((M + tile_bm(t) - 1) / tile_bm(t)) * ((N + tile_bn(t) - 1) / tile_bn(t));
@@ -51,7 +60,7 @@ inline int64_t tile_count(Tile t, int M, int N) {
 // tile weighs a little more than 128x128: per K slice it stages 320 operand
 // rows against 256, and on equal padded work (2048^3) 128x128 ran 13% faster.
 inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split,
-                       bool allow_groups = false) {
+                       bool allow_groups = false, bool allow_t = true) {
     Tile cands[4] = {Tile::L, Tile::W, Tile::M, Tile::S};
     const double eff[4] = {1.0, 1.25, 1.2, 1.6};
     Plan best{Tile::S, 1, std::max(K, 1)};
@@ -75,6 +84,20 @@ inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split,
         ks = (ks + kBK - 1) / kBK * kBK;
         best.splits = (K + ks - 1) / ks;
         best.k_split = ks;
+    }
+    if (allow_groups && allow_t && best.tile == Tile::S && tile_count(Tile::T, M, N) <= kNumCUs) {
+        // A small GEMM is bound by the operand bytes each CU streams (and
+        // their latency): 32x32 tiles in one round of the CUs halve them
+        // against 64x64 ones, with the K range unsplit (no reduce launch);
+        // wave groups over K keep several slices in flight.
+        const double cost_s = 128.0 * (best.splits > 1 ? best.k_split : K) +
+                              (best.splits > 1 ? kSplitReduceFloats : 0.0);
+        if (64.0 * K < cost_s) {
+            Plan t{Tile::T, 1, std::max(K, 1)};
+            const int slices = (K + kBK - 1) / kBK;
+            t.groups = slices >= 32 ? 8 : slices >= 16 ? 4 : slices >= 8 ? 2 : 1;
+            return t;
+        }
     }
     if (allow_groups && best.tile == Tile::S) {
         if (best.splits > 1 && best.splits <= kMaxGroupSplits) {
@@ -160,6 +183,7 @@ struct pipe_ok<P, std::void_t<decltype(P::kPipe)>> : std::bool_constant<P::kPipe
 
 template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t st) {
+    if (t == Tile::T && !pipe_ok<P>::value) return hipErrorInvalidValue;  // planned for pipe problems only
     if constexpr (ws_stream<P>::value) {
         // The 128x128 tile with warp-specialised producers (two waves per
         // block, two K slices in flight): 2048^3 in 33 us against 44 us on
@@ -177,6 +201,11 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
                 if (groups >= 4) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 4>(p, splits, st);
                 if (groups == 2) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
                 return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
+            case Tile::T:
+                if (groups >= 8) return launch_igemm_pipe<32, 32, 32, 1, 1, kPipeDepth, P, 8>(p, splits, st);
+                if (groups >= 4) return launch_igemm_pipe<32, 32, 32, 1, 1, kPipeDepth, P, 4>(p, splits, st);
+                if (groups == 2) return launch_igemm_pipe<32, 32, 32, 1, 1, kPipeDepth, P, 2>(p, splits, st);
+                return launch_igemm_pipe<32, 32, 32, 1, 1, kPipeDepth>(p, splits, st);
             default: break;
         }
     }
@@ -263,35 +292,67 @@ int run_plan(P p, const Plan& pl, hipStream_t st) {
     return SEERA_OK;
 }
 
-template <int KG, class P1, class P2>
+template <int BM, int KG, class P1, class P2>
 hipError_t launch_igemm_pipe_pair(const P1& p1, int nb1, const P2& p2, int nb2, hipStream_t st) {
-    using PC = PipeCfg<64, 64, 32, 2, 2, kPipeDepth, KG>;
-    auto kern = igemm_pipe_pair_kernel<64, 64, 32, 2, 2, kPipeDepth, KG, P1, P2>;
+    constexpr int WG = BM / 32;  // 2x2 waves of 32x32 on 64x64 tiles, one wave on 32x32
+    using PC = PipeCfg<BM, BM, 32, WG, WG, kPipeDepth, KG>;
+    auto kern = igemm_pipe_pair_kernel<BM, BM, 32, WG, WG, kPipeDepth, KG, P1, P2>;
     static_assert(PC::LDS_BYTES <= 65536, "the pair kernel's LDS fits the default limit");
     hipLaunchKernelGGL(kern, dim3((unsigned)(nb1 + nb2)), dim3(PC::NT), PC::LDS_BYTES, st, p1, p2,
                        nb1);
     return hipGetLastError();
 }
 
-// Runs two independent problems: in one launch when both plans are unsplit
-// 64x64 pipelined tiles and together fill at most one round of the CUs (the
+// Both plans of a pair on one small tile (32x32 or 64x64), unsplit, together
+// within one round of the CUs: the pair runs as one launch.
+inline bool pair_fits(const Plan& pl1, int M1, int N1, const Plan& pl2, int M2, int N2) {
+    return pl1.tile == pl2.tile && (pl1.tile == Tile::S || pl1.tile == Tile::T) && pl1.splits == 1 &&
+           pl2.splits == 1 && tile_count(pl1.tile, M1, N1) + tile_count(pl2.tile, M2, N2) <= kNumCUs;
+}
+
+// Plans of two independent GEMMs (a backward's dA and dB). When their best
+// plans do not pair and one of them is a 32x32 plan, both retry on 64x64
+// tiles (one launch costs less than the smaller tile saves); returns whether
+// the plans pair, and leaves each GEMM's own best plan when they do not.
+inline bool pair_plans(int M1, int N1, int K1, int M2, int N2, int K2, Plan& pl1, Plan& pl2) {
+    pl1 = plan_tiles(M1, N1, K1, true, true, true);
+    pl2 = plan_tiles(M2, N2, K2, true, true, true);
+    if (pair_fits(pl1, M1, N1, pl2, M2, N2)) return true;
+    if (pl1.tile != Tile::T && pl2.tile != Tile::T) return false;
+    const Plan q1 = plan_tiles(M1, N1, K1, true, true, true, false);
+    const Plan q2 = plan_tiles(M2, N2, K2, true, true, true, false);
+    if (!pair_fits(q1, M1, N1, q2, M2, N2)) return false;
+    pl1 = q1;
+    pl2 = q2;
+    return true;
+}
+
+// Runs two independent problems: in one launch when pair_fits (the
 // wave-group count of the two plans, the larger one, serves both), else one
 // after the other.
 template <bool BIG1, bool BIG2, class P1, class P2>
 int run_plan_pair(P1 p1, const Plan& pl1, P2 p2, const Plan& pl2, hipStream_t st) {
     if constexpr (pipe_ok<P1>::value && pipe_ok<P2>::value) {
-        const int64_t nb1 = tile_count(Tile::S, p1.M, p1.N), nb2 = tile_count(Tile::S, p2.M, p2.N);
-        if (pl1.tile == Tile::S && pl2.tile == Tile::S && pl1.splits == 1 && pl2.splits == 1 &&
-            nb1 + nb2 <= kNumCUs) {
-            p1.tiles_n = (p1.N + 63) / 64;
-            p2.tiles_n = (p2.N + 63) / 64;
+        if (pair_fits(pl1, p1.M, p1.N, pl2, p2.M, p2.N)) {
+            const Tile t = pl1.tile;
+            const int bm = tile_bm(t);
+            const int64_t nb1 = tile_count(t, p1.M, p1.N), nb2 = tile_count(t, p2.M, p2.N);
+            p1.tiles_n = (p1.N + bm - 1) / bm;
+            p2.tiles_n = (p2.N + bm - 1) / bm;
             p1.k_split = std::max(p1.K, 1);
             p2.k_split = std::max(p2.K, 1);
             p1.gm = p2.gm = 4;
             const int g = std::max(pl1.groups, pl2.groups);
-            hipError_t e = g >= 4   ? launch_igemm_pipe_pair<4>(p1, (int)nb1, p2, (int)nb2, st)
-                           : g == 2 ? launch_igemm_pipe_pair<2>(p1, (int)nb1, p2, (int)nb2, st)
-                                    : launch_igemm_pipe_pair<1>(p1, (int)nb1, p2, (int)nb2, st);
+            hipError_t e;
+            if (t == Tile::T)
+                e = g >= 8   ? launch_igemm_pipe_pair<32, 8>(p1, (int)nb1, p2, (int)nb2, st)
+                    : g >= 4 ? launch_igemm_pipe_pair<32, 4>(p1, (int)nb1, p2, (int)nb2, st)
+                    : g == 2 ? launch_igemm_pipe_pair<32, 2>(p1, (int)nb1, p2, (int)nb2, st)
+                             : launch_igemm_pipe_pair<32, 1>(p1, (int)nb1, p2, (int)nb2, st);
+            else
+                e = g >= 4   ? launch_igemm_pipe_pair<64, 4>(p1, (int)nb1, p2, (int)nb2, st)
+                    : g == 2 ? launch_igemm_pipe_pair<64, 2>(p1, (int)nb1, p2, (int)nb2, st)
+                             : launch_igemm_pipe_pair<64, 1>(p1, (int)nb1, p2, (int)nb2, st);
             if (e != hipSuccess) return fail_hip(e, "igemm pair launch");
             return SEERA_OK;
         }
