@@ -776,6 +776,9 @@ def main():
         extras["alloc_path"] = bench_alloc()
         extras["maxpool_2x2_s2"] = bench_maxpool(20, 3, stream, 2, 2, 0)
         extras["maxpool_3x3_s2_p1"] = bench_maxpool(20, 3, stream, 3, 2, 1)
+        # Layer shapes beyond the configs: [ms forward, ms backward] each.
+        extras["conv_layers"] = bench_conv_layers(5, 2, stream)
+        extras["gemm_shapes"] = bench_gemm_shapes(5, 2, stream)
         out["extras"] = extras
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(n)
