@@ -93,8 +93,10 @@ int stride2_conv(const float* in, const float* W, float* out, int B, int C, int 
 int stream_conv(const BandConvArgs& band, hipStream_t st, bool* used);
 
 // Three-role row streaming (conv_split.hip) of a 3x3, stride 1, pad 1 launch
-// of 64 input channels and width W <= 56 (W % 4 == 0): the matrix-core waves
-// hand their results to storer waves through LDS; *used reports whether it ran.
+// of 64k input channels (W % 4 == 0; rows wider than 56 in column tiles; one
+// launch per 64-channel slice, each after the first adding to the output):
+// the matrix-core waves hand their results to storer waves through LDS;
+// *used reports whether it ran.
 int split_conv(const BandConvArgs& band, hipStream_t st, bool* used);
 
 }  // namespace seera

@@ -5,6 +5,10 @@
 //   out[b, f, oh, ow] = sum_{c, t, u} Wk[f, t, u, c] * in[b, c, oh + t - 1, ow + u - 1]
 // (convolution.cu:15-101 forward; convolution.cu:144-265 dX).
 //
+// Inputs of more than 64 channels (a multiple of 64) run as one launch per
+// 64-channel slice, each after the first adding its sums to the output it
+// finds (the fused epilogue on the last one).
+//
 // A block owns one image, a strip of L output rows, up to 56 columns (rows
 // wider than that run as column tiles, each ring row holding the tile's
 // columns and one quad of halo on either side) and 64 filters, and walks the
@@ -76,8 +80,10 @@ constexpr int kStoreItems = 7;             // staged float4s per storer thread (
 static_assert(kPreW * kNT == kWPieces, "the weight pieces divide evenly over the block");
 
 struct SplitArgs {
-    const float* in;     // [B, 64, H, W] fp32
-    const half_t* wk;    // prepared fp16 weights (conv_band.hip layout), 64-filter tiles
+    const float* in;     // 64 input channels of image b at in + b * in_bstride ([64, H, W] fp32)
+    int64_t in_bstride;  // floats per input image (C * H * W)
+    const half_t* wk;    // prepared fp16 weights (conv_band.hip layout) of those 64 channels
+    int64_t wk_fstride;  // halves per 64-filter tile of wk
     float* out;          // [B, F, H, W] fp32
     int B, H, W, F;
     int L, nstrip;       // output rows per strip, strips per image
@@ -89,7 +95,9 @@ struct SplitArgs {
 
 constexpr int kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2;
 
-template <int EPI>
+// ACC: out += this launch's sums (a later 64-channel pass of a wider input;
+// the epilogue, if any, applies to the total).
+template <int EPI, bool ACC>
 __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     extern __shared__ __attribute__((aligned(16))) half_t smem[];
     const int ct = blockIdx.x % a.ncol, bs = blockIdx.x / a.ncol;
@@ -109,7 +117,7 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int HW = a.H * a.W;
-    const rsrc_t src = make_rsrc(a.in + (int64_t)b * 64 * HW);
+    const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.in_bstride);
     const uint32_t cstride = (uint32_t)(HW * 4);
     const int row_items = 8 * a.nq;            // (plane, 8-channel group, column quad) per row
 
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
 
     // ---- prologue, by all waves: the weights and strip input rows 0..3 ----
     {
-        const half_t* wsrc = a.wk + (int64_t)ftile * kWPieces * 8;
+        const half_t* wsrc = a.wk + (int64_t)ftile * a.wk_fstride;
         half8 wv[kPreW];
 #pragma unroll
         for (int k = 0; k < kPreW; ++k) wv[k] = *reinterpret_cast<const half8*>(wsrc + (int64_t)(k * kNT + tid) * 8);
@@ -278,6 +286,8 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
                 const uint32_t off = o < Lb && f < a.F && c0 + 4 * sq[k] < a.W
                     ? (uint32_t)(((f * a.H + ohA + o) * a.W + c0 + 4 * sq[k]) * 4) : kBufOOB;
                 floatx4_t x = v[k];
+                if constexpr (ACC)
+                    x += __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(dst_img, off, 0, 0));
                 if constexpr (EPI != kEpiNone) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -298,9 +308,9 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     }
 }
 
-template <int EPI>
+template <int EPI, bool ACC>
 hipError_t launch(const SplitArgs& a, int nblocks, int nftiles, int lds, hipStream_t st) {
-    auto kern = split_conv_kernel<EPI>;
+    auto kern = split_conv_kernel<EPI, ACC>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
@@ -312,8 +322,10 @@ hipError_t launch(const SplitArgs& a, int nblocks, int nftiles, int lds, hipStre
 
 int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     *used = false;
-    if (band.nphase != 1 || band.C != 64 || band.nchunks != 2 || band.ish != 1 || band.isw != 1 ||
-        band.osh != 1 || band.osw != 1)
+    // Inputs of 64k channels run as k launches over 64-channel slices, each
+    // after the first adding its sums to the output.
+    if (band.nphase != 1 || band.C < 64 || band.C % 64 != 0 || band.nchunks != band.C / 32 ||
+        band.ish != 1 || band.isw != 1 || band.osh != 1 || band.osw != 1)
         return SEERA_OK;
     const BandPhase& P = band.ph[0];
     if (P.T != 3 || P.U != 3 || P.iph != 1 || P.ipw != 1 || P.oph != 0 || P.opw != 0 || P.woff != 0)
@@ -325,8 +337,19 @@ int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     if ((int64_t)64 * band.H * band.W * 4 > kMaxTileSpanBytes ||
         (int64_t)band.F * band.H * band.W * 4 > kMaxTileSpanBytes)
         return SEERA_OK;
+    // Each further slice reads and rewrites the output once more: against the
+    // band kernel, measured faster up to 4 (slice, filter tile) launches on
+    // rows of 56 or more (16x128x112^2 -> 128: 160 -> 114 us; 64x128x56^2 ->
+    // 128: 150 -> 109) or with one filter tile (32x192x28^2 -> 64: 46 -> 36),
+    // slower on 28-column rows with two filter tiles (45 -> 52) and at 256
+    // channels and filters (137 -> 185 at 28^2, 73 -> 91 at 56^2).
+    const int npass = band.C / 64;
+    if (npass > 1 && !(npass * band.nftiles <= 4 && (band.W >= 56 || band.nftiles == 1)))
+        return SEERA_OK;
     SplitArgs a{};
     a.in = band.in; a.wk = band.wk; a.out = band.out; a.epi = band.epi;
+    a.in_bstride = (int64_t)band.C * band.H * band.W;
+    a.wk_fstride = (int64_t)band.nchunks * 9 * 2048;
     a.B = band.B; a.H = band.H; a.W = band.W; a.F = band.F;
     // Rows wider than 56 run as column tiles of at most 56 (the ring holds a
     // tile's columns plus a quad of halo on each side).
@@ -349,11 +372,25 @@ int split_conv(const BandConvArgs& band, hipStream_t st, bool* used) {
     a.nstrip = (a.H + a.L - 1) / a.L;
     const int64_t nblocks = (int64_t)a.B * a.nstrip * a.ncol;
     if (nblocks > 0x7fffffff || band.nftiles > 65535) return SEERA_OK;
-    hipError_t e;
-    if (a.epi.act == kActRelu) e = launch<kEpiBiasRelu>(a, (int)nblocks, band.nftiles, lds, st);
-    else if (a.epi.bias) e = launch<kEpiBias>(a, (int)nblocks, band.nftiles, lds, st);
-    else e = launch<kEpiNone>(a, (int)nblocks, band.nftiles, lds, st);
-    if (e != hipSuccess) return fail_hip(e, "split conv launch");
+    const ConvEpi epi = band.epi;
+    for (int pass = 0; pass < npass; ++pass) {
+        SplitArgs q = a;
+        q.in = band.in + (int64_t)pass * 64 * band.H * band.W;
+        q.wk = band.wk + (int64_t)pass * 2 * 9 * 2048;  // chunks 2*pass, 2*pass + 1 of each tile
+        q.epi = pass + 1 == npass ? epi : ConvEpi{};   // the epilogue on the total only
+        const bool acc = pass > 0;
+        hipError_t e;
+        if (q.epi.act == kActRelu)
+            e = acc ? launch<kEpiBiasRelu, true>(q, (int)nblocks, band.nftiles, lds, st)
+                    : launch<kEpiBiasRelu, false>(q, (int)nblocks, band.nftiles, lds, st);
+        else if (q.epi.bias)
+            e = acc ? launch<kEpiBias, true>(q, (int)nblocks, band.nftiles, lds, st)
+                    : launch<kEpiBias, false>(q, (int)nblocks, band.nftiles, lds, st);
+        else
+            e = acc ? launch<kEpiNone, true>(q, (int)nblocks, band.nftiles, lds, st)
+                    : launch<kEpiNone, false>(q, (int)nblocks, band.nftiles, lds, st);
+        if (e != hipSuccess) return fail_hip(e, "split conv launch");
+    }
     *used = true;
     return SEERA_OK;
 }

@@ -67,6 +67,15 @@ CONV2D_STREAM = [
     # 64 channels on rows wider than 56: the three-role forward in column tiles
     ("s18", 1, 64, 6, 60, 64, 3, 3, 1, 1),     # 2 tiles of 32 (the second 28 wide)
     ("s19", 2, 64, 5, 200, 40, 3, 3, 1, 1),    # 4 tiles of 52 (the last 44), partial filter tile
+    # more than 64 channels on the three-role kernel: one launch per
+    # 64-channel slice, each after the first adding to the output (up to 4
+    # slice x filter-tile launches, two filter tiles on rows of 56 or more)
+    ("m01", 2, 128, 12, 16, 64, 3, 3, 1, 1),   # forward in 2 slices
+    ("m02", 1, 192, 6, 60, 64, 3, 3, 1, 1),    # 3 slices, column tiles
+    ("m03", 2, 64, 8, 8, 128, 3, 3, 1, 1),     # dX over 128 dY channels: 2 slices
+    ("m04", 1, 256, 5, 20, 64, 3, 3, 1, 1),    # 4 slices
+    ("m05", 1, 128, 6, 60, 96, 3, 3, 1, 1),    # 2 slices x 2 filter tiles (the second partial)
+    ("m06", 1, 128, 4, 64, 128, 3, 3, 1, 1),   # 2 x 2, forward and dX
 ]
 
 # Edge shapes (not from the reference's tests): 1x1 image and kernel, channel

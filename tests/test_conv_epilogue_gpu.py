@@ -33,6 +33,7 @@ SHAPES = [
     ("gather_1f", 4, 8, 9, 9, 1, 3, 1, 1),         # one filter
     ("conv1x1", 3, 32, 10, 12, 24, 1, 1, 0),       # 1x1 projection
     ("s2d_7x7", 2, 3, 16, 16, 8, 7, 2, 3),         # 7x7 s2: space-to-depth form
+    ("slices_128", 2, 128, 10, 12, 70, 3, 1, 1),   # 2 channel slices: epilogue on the total
 ]
 
 
