@@ -269,6 +269,23 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
         const int fg = ftile * 64 + (fr >> 1);
         sbias[k] = EPI != kEpiNone && a.epi.bias && sf[k] >= 0 && fg < a.F ? a.epi.bias[fg] : 0.f;
     }
+    // Output offset of item k of step st (kBufOOB past the strip or tile).
+    auto item_off = [&](int st, int k) {
+        const int o = 2 * st + sr[k], f = ftile * 64 + sf[k];
+        return o < Lb && f < a.F && c0 + 4 * sq[k] < a.W
+            ? (uint32_t)(((f * a.H + ohA + o) * a.W + c0 + 4 * sq[k]) * 4) : kBufOOB;
+    };
+    // ACC: the output's current values of the items of the next step to
+    // store, requested a step ahead (loads issued after a store of the same
+    // buffer would otherwise each wait out the store before them).
+    floatx4_t old[kStoreItems];
+    auto load_old = [&](int st) {
+#pragma unroll
+        for (int k = 0; k < kStoreItems; ++k)
+            old[k] = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         dst_img, sf[k] >= 0 ? item_off(st, k) : kBufOOB, 0, 0));
+    };
+    if constexpr (ACC) load_old(0);
     for (int s = 0; s <= nsteps; ++s) {
         if (s > 0) {
             const int st = s - 1;  // the staged step
@@ -282,12 +299,9 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
 #pragma unroll
             for (int k = 0; k < kStoreItems; ++k) {
                 if (sf[k] < 0) continue;
-                const int o = 2 * st + sr[k], f = ftile * 64 + sf[k];
-                const uint32_t off = o < Lb && f < a.F && c0 + 4 * sq[k] < a.W
-                    ? (uint32_t)(((f * a.H + ohA + o) * a.W + c0 + 4 * sq[k]) * 4) : kBufOOB;
+                const uint32_t off = item_off(st, k);
                 floatx4_t x = v[k];
-                if constexpr (ACC)
-                    x += __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(dst_img, off, 0, 0));
+                if constexpr (ACC) x += old[k];
                 if constexpr (EPI != kEpiNone) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -303,6 +317,8 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4_t, m), mask_img, off, 0, 0);
                 }
             }
+            if constexpr (ACC)
+                if (st + 1 < nsteps) load_old(st + 1);
         }
         if (s < nsteps) __syncthreads();  // B(s+1)
     }
