@@ -303,8 +303,11 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
                 bb = u / a.vP;                                                             \
                 ih = u - bb * a.vP - a.ph;                                                 \
             }                                                                              \
+            /* (virtual rows: the last strip's X rows run R - 1 rows past    \
+               the batch's last period, into an image bb = B that is not     \
+               there) */                                                      \
             const bool rok = xrow[k] < (NX) && (unsigned)i < (unsigned)need &&             \
-                             (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C;            \
+                             (unsigned)ih < (unsigned)a.H && c0 + xch[k] < a.C && bb < a.B; \
             const int xrb = (bb * a.C * a.H + ih) * a.W * 4;                               \
             uint32_t xo[3];                                                                \
             _Pragma("unroll") for (int q = 0; q < 3; ++q)                                  \

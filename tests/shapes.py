@@ -64,6 +64,9 @@ CONV2D_STREAM = [
     ("s15", 65, 128, 4, 4, 256, 3, 3, 1, 1),   # 8 tiles, rows of 4 + 2 per image
     ("s16", 130, 64, 5, 8, 256, 3, 3, 1, 1),   # odd image height
     ("s17", 520, 16, 3, 8, 16, 1, 3, 1, 1),    # 1x3: no extra rows per image
+    # the last strip's X rows run past the batch's last period: they must
+    # read nothing (X ends where its allocation ends)
+    ("s20", 64, 256, 14, 16, 256, 3, 3, 1, 1),
     # 64 channels on rows wider than 56: the three-role forward in column tiles
     ("s18", 1, 64, 6, 60, 64, 3, 3, 1, 1),     # 2 tiles of 32 (the second 28 wide)
     ("s19", 2, 64, 5, 200, 40, 3, 3, 1, 1),    # 4 tiles of 52 (the last 44), partial filter tile
