@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kNT) void band_conv_pipe(const BandConvArgs a) {
     const int nq = a.BC4 >> 2;
     const int band_items = a.BR * nq * 4;
     const half_t* wsrc_base = a.wk + P.woff + (int64_t)ftile * a.nchunks * taps * 2048;
-    const rsrc_t isrc = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+    const rsrc_t isrc = make_rsrc_in(a.in, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W);
     const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
     // Per item: (row, quad, 8-channel group); the byte offset of its first
     // element at channel 0 (kBufOOB: outside the image) and its band pixel.
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
         const int item = it0 + (J) / NCH, ch = (J) % NCH;                                   \
         const int b = tile_b(item), oh0 = tile_oh0(item), ow0 = tile_ow0(item);             \
         if (ch == 0) {                                                                      \
-            const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + ftile * 64) * a.Ho * a.Wo); \
+            const rsrc_t dsrc = make_rsrc_in(a.dy, (int64_t)a.B * a.F * a.Ho * a.Wo, ((int64_t)b * a.F + ftile * 64) * a.Ho * a.Wo); \
             _Pragma("unroll") for (int kk = 0; kk < kWgDyMax; ++kk) {                       \
                 const int fl = dyit[kk] & 255, ohl = (dyit[kk] >> 8) & 255, m = dyit[kk] >> 16; \
                 const int oh = oh0 + ohl, ow = ow0 + 8 * m;                                 \
@@ -822,7 +822,7 @@ __global__ __launch_bounds__(kWgNT) void band_wgrad_kernel(const WgradArgs a) {
             const int c = ctile * a.CT + ch * 32 + cl, hin = oh0 * a.sh - a.ph + row;       \
             const int a0 = floor4(ow0 * a.sw - a.pw) + 8 * XI::OCT * grp * SW;              \
             const bool rowok = xit >= 0 && c < a.C && (unsigned)hin < (unsigned)a.H;        \
-            const rsrc_t xsrc = make_rsrc(a.x + (int64_t)b * a.C * a.H * a.W);              \
+            const rsrc_t xsrc = make_rsrc_in(a.x, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W); \
             const int rbase = rowok ? (c * a.H + hin) * a.W : 0;                            \
             _Pragma("unroll") for (int q = 0; q < 11; ++q) {                                \
                 const int col = a0 + 4 * q;                                                 \

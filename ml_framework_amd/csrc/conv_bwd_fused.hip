@@ -130,8 +130,9 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
     const int ptid = tid - kCons;
     const int HW = a.H * a.W;
     const uint32_t cstride = (uint32_t)(HW * 4);
-    const rsrc_t ysrc = make_rsrc(a.dy + (int64_t)b * 64 * HW);
-    const rsrc_t xsrc = make_rsrc(a.x + (int64_t)b * 64 * HW);
+    const int64_t total = (int64_t)a.B * 64 * HW;
+    const rsrc_t ysrc = make_rsrc_in(a.dy, total, (int64_t)b * 64 * HW);
+    const rsrc_t xsrc = make_rsrc_in(a.x, total, (int64_t)b * 64 * HW);
     // Items (8 channels x 4 columns) per row: X rows hold the tile's QW
     // quads, dY rows HQ more quads of halo on either side.
     const int QY = a.QW + 2 * a.HQ;
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(kNT) void fused_bwd_kernel(const FusedArgs a) {
 #pragma unroll
         for (int u = 0; u < 3; ++u) oa[u] = ring_off(32 * pxh + (lane & 15) + u + kYPad - 1, kc);
         const int ob = w_off(lane & 15, kc) + 512 * 2 * chh;  // + 512 * cs
-        const rsrc_t dxdst = make_rsrc(a.dx + (int64_t)b * 64 * HW);
+        const rsrc_t dxdst = make_rsrc_in(a.dx, total, (int64_t)b * 64 * HW);
 
         floatx4_t acc[2][3][3];
 #pragma unroll

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
     const int g0 = a.ne - 1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+    const rsrc_t src = make_rsrc_in(a.in, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W);
     const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
     const int row_items = NCH * 4 * nq;           // items per input row
     const int need = Lb + a.ne - 1;               // strip input rows used
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(kNT) void phase2_conv_kernel(const Phase2Args a) {
     // tile only at its end.
     const int npq = min(2 * kWC, a.Wout - 2 * ow0) >> 3;
     const int nst_items = 4 * 32 * npq;
-    const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Hout * a.Wout);
+    const rsrc_t dst_img = make_rsrc_in(a.out, (int64_t)a.B * a.F * a.Hout * a.Wout, (int64_t)b * a.F * a.Hout * a.Wout);
     auto flush = [&](int st) {  // phase rows 2st, 2st + 1: output rows 4st .. 4st + 3
 #pragma unroll
         for (int k = 0; k < kStageItems; ++k) {

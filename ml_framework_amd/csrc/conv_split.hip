@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int HW = a.H * a.W;
-    const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.in_bstride);
+    const rsrc_t src = make_rsrc_in(a.in, (int64_t)(a.B - 1) * a.in_bstride + 64 * HW, (int64_t)b * a.in_bstride);
     const uint32_t cstride = (uint32_t)(HW * 4);
     const int row_items = 8 * a.nq;            // (plane, 8-channel group, column quad) per row
 
@@ -252,8 +252,9 @@ __global__ __launch_bounds__(kNT) void split_conv_kernel(const SplitArgs a) {
     // last barrier those of the last step ----
     const int stid = tid - 2 * kWaves * 64;
     const int nitems = 2 * 64 * a.nqo;
-    const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * HW);
-    const rsrc_t mask_img = make_rsrc(EPI == kEpiBiasRelu && a.epi.mask ? a.epi.mask + (int64_t)b * a.F * HW : a.out);
+    const int64_t out_n = (int64_t)a.B * a.F * HW, out_o = (int64_t)b * a.F * HW;
+    const rsrc_t dst_img = make_rsrc_in(a.out, out_n, out_o);
+    const rsrc_t mask_img = make_rsrc_in(EPI == kEpiBiasRelu && a.epi.mask ? a.epi.mask : a.out, out_n, out_o);
     const bool mask_on = EPI == kEpiBiasRelu && a.epi.mask;
     // item k: index (k * 256 + stid) = (f * 2 + r) * nqo + q, quads fastest:
     // two output rows of a filter plane are contiguous in HBM

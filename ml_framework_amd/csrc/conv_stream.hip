@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         }
         // Items as the producers' (row, chunk, 8-channel group cg, column
         // quad q4), cg fastest, over strip input rows [-sh, g0 + kG).
-        const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+        const rsrc_t src = make_rsrc_in(a.in, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W);
         const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
         const int row_items = a.nchunks * 4 * nq;
         const int nitems = (g0 + sh + kG) * row_items;  // <= kPreItems * kNT (host check)
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         const int nqt = a.nchunks * taps;
         // Output: buffer resource over this image's [F, Hout, Wout] block;
         // lanes outside the tile get kBufOOB and their stores are dropped.
-        const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Hout * a.Wout);
+        const rsrc_t dst_img = make_rsrc_in(a.out, (int64_t)a.B * a.F * a.Hout * a.Wout, (int64_t)b * a.F * a.Hout * a.Wout);
         const int hw = a.Hout * a.Wout;
         const int fl = ftile * 64 + (lane & 15);  // filter of this lane (+ fg*16)
         // Fused epilogue (the bias and ReLU of a Conv2D layer): bias of each of
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
         for (int fg = 0; fg < 4; ++fg)
             bv[fg] = a.epi.bias && fl + fg * 16 < a.F ? a.epi.bias[fl + fg * 16] : 0.f;
         const rsrc_t mask_img =
-            make_rsrc(mask_on ? a.epi.mask + (int64_t)b * a.F * a.Hout * a.Wout : a.out);
+            make_rsrc_in(mask_on ? a.epi.mask : a.out, (int64_t)a.B * a.F * a.Hout * a.Wout, (int64_t)b * a.F * a.Hout * a.Wout);
         auto finish = [&](floatx4_t v, int fg) {
             if constexpr (EPI != kEpiNone) {
 #pragma unroll
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kNT) void stream_conv_kernel(const StreamArgs a) {
     // kMaxTileSpanBytes and that C is a multiple of 8, so an item's 8 channels
     // are all in range or all out).
     const int ptid = tid - kCons;
-    const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+    const rsrc_t src = make_rsrc_in(a.in, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W);
     const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
     const int row_items = a.nchunks * 4 * nq;    // items per input row
     const int need = Lb + T - 1;                 // strip-relative input rows used

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kNT) void stride2_conv_kernel(const Stride2Args a) 
     // step g-1) is rows 4g+2 .. 4g+5, the prologue writes rows 0..5.
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const rsrc_t src = make_rsrc(a.in + (int64_t)b * a.C * a.H * a.W);
+    const rsrc_t src = make_rsrc_in(a.in, (int64_t)a.B * a.C * a.H * a.W, (int64_t)b * a.C * a.H * a.W);
     const uint32_t cstride = (uint32_t)(a.H * a.W * 4);
     constexpr int nq = kBC / 2;                   // column quads per input row
     constexpr int row_items = NCH * 4 * nq;       // items per input row
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kNT) void stride2_conv_kernel(const Stride2Args a) 
         }
         const int kc = lane >> 4;
         const int f = ftile * 64 + wave * 16 + (lane & 15);
-        const rsrc_t dst_img = make_rsrc(a.out + (int64_t)b * a.F * a.Ho * a.Wo);
+        const rsrc_t dst_img = make_rsrc_in(a.out, (int64_t)a.B * a.F * a.Ho * a.Wo, (int64_t)b * a.F * a.Ho * a.Wo);
         const int hw = a.Ho * a.Wo;
         // Frames: tap s = 0: O pixel x+1, s = 1: E x+2, s = 2: O x+2, s = 3: E x+3
         // (x = output column - ow0); [s][pixel group] offsets within a row.

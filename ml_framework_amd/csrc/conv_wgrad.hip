@@ -248,8 +248,8 @@ __global__ __launch_bounds__(kNT) void stream_wgrad_kernel(const WStreamArgs a) 
     // columns, channels and filters read 0.
     const int ptid = tid - kCons;
     const int c0 = ctile * kTile, f0 = ftile * kTile;
-    const rsrc_t xsrc = make_rsrc(a.x + ((int64_t)b * a.C + c0) * a.H * a.W);
-    const rsrc_t dsrc = make_rsrc(a.dy + ((int64_t)b * a.F + f0) * a.Ho * a.Wo);
+    const rsrc_t xsrc = make_rsrc_in(a.x, (int64_t)a.B * a.C * a.H * a.W, ((int64_t)b * a.C + c0) * a.H * a.W);
+    const rsrc_t dsrc = make_rsrc_in(a.dy, (int64_t)a.B * a.F * a.Ho * a.Wo, ((int64_t)b * a.F + f0) * a.Ho * a.Wo);
     const int nxo = (a.Wp >> 3) + 1;             // X octets per ring row
     const int ndo = a.Wp >> 3;                   // dY octets per ring row
     const int dd = DD >= 0 ? DD : ((-a.pw) % 4 + 4) % 4;

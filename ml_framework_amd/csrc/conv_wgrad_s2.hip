@@ -156,8 +156,8 @@ __global__ __launch_bounds__(kNT) void wgrad_s2_kernel(const WgradS2Args a) {
         const int ow0 = cb * kWC;
         const int need = 2 * Lb + 2;              // strip input rows used
         const int hin0 = 2 * oh0 - 1;             // image row of strip input row 0
-        const rsrc_t ysrc = make_rsrc(a.y + ((int64_t)b * a.F + ftile * 64) * a.Ho * a.Wo);
-        const rsrc_t xsrc = make_rsrc(a.x + ((int64_t)b * a.C + c_base) * a.H * a.W);
+        const rsrc_t ysrc = make_rsrc_in(a.y, (int64_t)a.B * a.F * a.Ho * a.Wo, ((int64_t)b * a.F + ftile * 64) * a.Ho * a.Wo);
+        const rsrc_t xsrc = make_rsrc_in(a.x, (int64_t)a.B * a.C * a.H * a.W, ((int64_t)b * a.C + c_base) * a.H * a.W);
 
         floatx4 yv[2][2];
         floatx4 xv[CG][6];

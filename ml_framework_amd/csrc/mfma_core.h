@@ -58,6 +58,16 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
                                              0x00020000);
 }
 
+// A buffer resource at element `off` of a tensor of `total` floats covering
+// the rest of the tensor (capped at kBufRecords bytes): a load past the
+// tensor's end reads 0 and a store there is dropped, so an offset that leaves
+// the tensor cannot fault.
+__device__ __forceinline__ rsrc_t make_rsrc_in(const float* tensor, int64_t total, int64_t off) {
+    const int64_t bytes = (total - off) * 4;
+    const uint32_t n = bytes <= 0 ? 0u : bytes >= (int64_t)kBufRecords ? kBufRecords : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(tensor + off), (short)0, n, 0x00020000);
+}
+
 __device__ __forceinline__ floatx4 buf_load4(rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
