@@ -203,6 +203,9 @@ MATMUL = [
     # few tiles: four wave groups in place of split-K, the last group's part
     # one slice or a K tail
     (256, 400, 256, 1), (256, 500, 256, 1),
+    # 32x32 tiles (one wave per K group): 8, 4 and 2 groups, a scalar-load B,
+    # a backward pair on 32x32 tiles and one that retries on 64x64 ones
+    (64, 1200, 64, 1), (96, 1536, 96, 1), (160, 600, 72, 1), (50, 300, 30, 2),
 ]
 
 # Testing/test_1.py:309-340 -- (name, N, C, H, W, KH, KW, stride, pad), MaxPool2D

@@ -35,6 +35,8 @@ SHAPES = [
     (7, 0, 5, 1),          # K = 0: C = act(bias)
     (4096, 4096, 512, 1),  # 256x256 warp-specialised tiles
     (2049, 2047, 1025, 1),  # unaligned and large: zero-padded staging copies of A and B
+    (64, 1200, 64, 1),     # 32x32 tiles, 8 wave groups
+    (50, 300, 30, 2),      # 32x32 tiles, scalar-load B, folded batch
 ]
 
 
@@ -111,6 +113,7 @@ BWD_SHAPES = [
     (2048, 2048, 2048, 1),  # 256x256 warp-specialised tiles
     (2049, 2047, 1025, 1),  # unaligned and large: zero-padded staging copies
     (5, 0, 7, 1),          # K = 0: empty dA and dB
+    (160, 600, 72, 1),     # dA + dB as one launch on 32x32 tiles
 ]
 
 
