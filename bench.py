@@ -620,6 +620,7 @@ WORKLOADS = {
     "gemm1024": lambda steps, warmup, st: bench_gemm(1024, steps, warmup, st, True),
     "gemm2048": lambda steps, warmup, st: bench_gemm(2048, steps, warmup, st, True),
     "gemm4096": lambda steps, warmup, st: bench_gemm(4096, steps, warmup, st, False),
+    "gemm4096_fwd_bwd": lambda steps, warmup, st: bench_gemm(4096, steps, warmup, st, True),
     "gemm8192": lambda steps, warmup, st: bench_gemm(8192, steps, warmup, st, False),
     "mlp_cfg3": bench_mlp,
     "conv2d_cfg4": bench_conv,

@@ -659,4 +659,108 @@ hipError_t launch_igemm_ws2(const P& p, int splits, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// igemm_ws2_kernel with one producer register set: slice s is rounded into
+// LDS and the same registers at once take the loads of slice s + 1 (one slice
+// of loads in flight), which leaves the registers for 64-deep slices (half as
+// many barriers per K as 32-deep ones).
+template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>
+__global__ __launch_bounds__((CWM * CWN + NPW) * 64) void igemm_ws1_kernel(const P p) {
+    using Cfg = WsCfg<BM, BN, BK, CWM, CWN, NPW>;
+    constexpr int NC = Cfg::NC, NP = Cfg::NP;
+    extern __shared__ __attribute__((aligned(16))) half_t smem[];
+    constexpr int STAGE = (BM + BN) * BK;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, p.tiles_n, p.gm, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = blockIdx.z * p.k_split;
+    const int kend = min(p.K, kbeg + p.k_split);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    constexpr bool CS = has_colsum<P>::value;
+    if (tid < NC) {
+        ws_consume<BM, BN, BK, CWM, CWN>(p, smem, m0, n0, nk, wave, lane);
+        if constexpr (CS) {
+            const float none[4] = {0.f, 0.f, 0.f, 0.f};
+            if (tm == 0) colsum_finish<BN, NP>(p, none, 0, -1, n0, blockIdx.z, smem);
+        }
+        return;
+    }
+
+    const int ptid = tid - NC;
+    float csum[4] = {0.f, 0.f, 0.f, 0.f};
+    if (nk > 0) {
+    using SA = typename P::template WA<BM, BK, NP>;
+    using SB = typename P::template WB<BN, BK, NP>;
+    SA sa;
+    SB sb;
+    p.ws_init_a(sa, m0, ptid);
+    p.ws_init_b(sb, n0, ptid);
+    if constexpr (CS) sb.colsum_begin(tm == 0);
+    typename SA::Regs ra;
+    typename SB::Regs rb;
+    auto kof = [&](int s) { return kbeg + min(s, nk - 1) * BK; };
+#define SEERA_WS_FENCE() __builtin_amdgcn_sched_barrier(0)
+    {
+        const int k0_ = kof(0);
+        const rsrc_t xa_ = sa.slice(k0_), xb_ = sb.slice(k0_);
+#pragma unroll
+        for (int q = 0; q < SA::PARTS; ++q) {
+            sa.load(ra, q, xa_);
+            SEERA_WS_FENCE();
+        }
+#pragma unroll
+        for (int q = 0; q < SB::PARTS; ++q) {
+            sb.load(rb, q, xb_);
+            SEERA_WS_FENCE();
+        }
+    }
+    for (int s = 0; s < nk; ++s) {
+        half_t* const st_ = smem + (s & 1) * STAGE;
+        const int k0_ = kof(s + 1);
+        const rsrc_t xa_ = sa.slice(k0_), xb_ = sb.slice(k0_);
+#pragma unroll
+        for (int q = 0; q < SA::PARTS; ++q) {
+            SEERA_WS_FENCE();
+            sa.store(ra, q, st_, ptid);
+            SEERA_WS_FENCE();
+            sa.load(ra, q, xa_);
+        }
+#pragma unroll
+        for (int q = 0; q < SB::PARTS; ++q) {
+            SEERA_WS_FENCE();
+            sb.store(rb, q, st_ + BM * BK, ptid);
+            SEERA_WS_FENCE();
+            sb.load(rb, q, xb_);
+        }
+        SEERA_WS_FENCE();
+        __syncthreads();  // releases slice s
+    }
+#undef SEERA_WS_FENCE
+    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (CS) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) csum[q] = sb.cs[q];
+    }
+    }
+    if constexpr (CS) {
+        using SBT = typename P::template WB<BN, BK, NP>;
+        if (tm == 0) colsum_finish<BN, NP>(p, csum, SBT::col0(ptid), SBT::slot(ptid), n0, blockIdx.z, smem);
+    }
+}
+
+template <int BM, int BN, int BK, int CWM, int CWN, int NPW, class P>
+hipError_t launch_igemm_ws1(const P& p, int splits, hipStream_t stream) {
+    using Cfg = WsCfg<BM, BN, BK, CWM, CWN, NPW>;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    dim3 grid(tiles_m * p.tiles_n, 1, splits);
+    auto kern = igemm_ws1_kernel<BM, BN, BK, CWM, CWN, NPW, P>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), Cfg::LDS_BYTES, stream, p);
+    return hipGetLastError();
+}
+
 }  // namespace seera

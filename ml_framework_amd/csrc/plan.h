@@ -216,6 +216,8 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
                     // Split sizes are multiples of kBK, so K % 32 == 0 makes
                     // every slice of every split whole.
                     static_assert(kBK % 32 == 0, "split-K granularity must be whole slices");
+                    if (p.K % 64 == 0 && p.k_split % 64 == 0)
+                        return launch_igemm_ws1<256, 256, 64, 4, 2, 4>(p, splits, st);
                     if (p.K % 32 == 0) return launch_igemm_ws2<256, 256, 32, 4, 2, 4>(p, splits, st);
                 }
                 return launch_igemm_ws<256, 256, 32, 4, 2, 4>(p, splits, st);

@@ -27,6 +27,7 @@ HIP_FILES = [s for s in hip_build.HIP_SOURCES if s.endswith(".hip")]
 MUST_SEE = [
     "fused_bwd_kernel",
     "igemm_ws2_kernel",
+    "igemm_ws1_kernel",
     "igemm_ws_kernel",
     "igemm_pipe_kernel",
     "stream_conv_kernel",
