@@ -732,7 +732,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic_from_profiles(),
-            "kernel": "igemm_ws2_kernel<256,256,32,4,2,4,GemmProblem> (GEMM fwd)",
+            "kernel": "igemm_ws1_kernel<256,256,64,4,2,4,GemmProblem> (GEMM fwd)",
             "algorithmic": "2*4096^3 FLOP per launch, one launch per step",
         },
         "parity": {"gemm_rel_fro_sampled": g["rel_fro_sampled"]},
