@@ -189,6 +189,8 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
         // block, two K slices in flight): 2048^3 in 33 us against 44 us on
         // the pipelined kernel below. The 64x64 and 64x256 tiles gain nothing
         // or spill with a single producer wave, and keep the pipelined kernel.
+        if (t == Tile::M && p.K % 64 == 0 && p.k_split % 64 == 0)
+            return launch_igemm_ws1<128, 128, 64, 2, 2, 2>(p, splits, st);
         if (t == Tile::M && p.K % 32 == 0)
             return launch_igemm_ws2<128, 128, 32, 2, 2, 2>(p, splits, st);
     }
