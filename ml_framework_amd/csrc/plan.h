@@ -190,7 +190,7 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
         // the pipelined kernel below. The 64x64 and 64x256 tiles gain nothing
         // or spill with a single producer wave, and keep the pipelined kernel.
         if (t == Tile::M && p.K % 64 == 0 && p.k_split % 64 == 0)
-            return launch_igemm_ws1<128, 128, 64, 2, 2, 2>(p, splits, st);
+            return launch_igemm_ws1<128, 128, 64, 2, 2, 4>(p, splits, st);
         if (t == Tile::M && p.K % 32 == 0)
             return launch_igemm_ws2<128, 128, 32, 2, 2, 2>(p, splits, st);
     }
