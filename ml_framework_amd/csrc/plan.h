@@ -185,10 +185,12 @@ template <bool BIG, class P>
 hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t st) {
     if (t == Tile::T && !pipe_ok<P>::value) return hipErrorInvalidValue;  // planned for pipe problems only
     if constexpr (ws_stream<P>::value) {
-        // The 128x128 tile with warp-specialised producers (two waves per
-        // block, two K slices in flight): 2048^3 in 33 us against 44 us on
-        // the pipelined kernel below. The 64x64 and 64x256 tiles gain nothing
-        // or spill with a single producer wave, and keep the pipelined kernel.
+        // The 128x128 tile with warp-specialised producers: four producer
+        // waves with one 64-deep slice in flight (2048^3 in 31 us) when K and
+        // the splits are whole 64-deep slices, else two producer waves with
+        // two 32-deep slices in flight (33 us; 44 us on the pipelined kernel
+        // below). The 64x64 and 64x256 tiles gain nothing or spill with a
+        // single producer wave, and keep the pipelined kernel.
         if (t == Tile::M && p.K % 64 == 0 && p.k_split % 64 == 0)
             return launch_igemm_ws1<128, 128, 64, 2, 2, 4>(p, splits, st);
         if (t == Tile::M && p.K % 32 == 0)
@@ -216,7 +218,9 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
             case Tile::L:
                 if constexpr (ws_stream<P>::value) {
                     // Split sizes are multiples of kBK, so K % 32 == 0 makes
-                    // every slice of every split whole.
+                    // every 32-deep slice of every split whole; 64-deep
+                    // slices (half the barriers per K) need K and the split
+                    // size to be multiples of 64.
                     static_assert(kBK % 32 == 0, "split-K granularity must be whole slices");
                     if (p.K % 64 == 0 && p.k_split % 64 == 0)
                         return launch_igemm_ws1<256, 256, 64, 4, 2, 4>(p, splits, st);
