@@ -1,4 +1,4 @@
-"""Conv2D and ConvTranspose2D forward/backward on seeded random shapes (not
+"""Conv2D, ConvTranspose2D and GEMM forward/backward on seeded random shapes (not
 from the reference's tests): channel counts, sizes, kernels, strides and
 paddings drawn over ranges that reach every dispatch path (three-role and
 row-streaming kernels, channel slices, column tiles, widened rows, stride
