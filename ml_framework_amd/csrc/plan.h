@@ -10,11 +10,11 @@
 namespace seera {
 
 // Block-tile shapes (BM x BN x BK, wave grid):
-//   L   256x256x32, warp-specialised: 4x2 consumer waves of 64x128 run the
-//       MFMAs while 4 producer waves load and round the next K slice
+//   L   256x256x64 (or x32), warp-specialised: 4x2 consumer waves of 64x128
+//       run the MFMAs while 4 producer waves load and round the next K slice
 //   W   64x256x32,  1x4 waves of 64x64  few rows (conv output channels)
-//   M   128x128x32, 2x2 waves of 64x64 (warp-specialised, 2 producer waves,
-//       when the operands take streaming stagers)
+//   M   128x128x64 (or x32), 2x2 waves of 64x64 (warp-specialised with 4 (or
+//       2) producer waves when the operands take streaming stagers)
 //   S   64x64x32,   2x2 waves of 32x32  small / odd shapes, scalar loads
 //   T   32x32x32,   one wave per K group  GEMMs whose 32x32 tiles fit one round
 //       of the CUs (half the operand bytes per CU of a 64x64 tile)
