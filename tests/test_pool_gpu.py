@@ -9,6 +9,8 @@ to closed forms computed with torch on the CPU: values against max_pool2d on
 the -inf-padded input, the mask against its argmax indices (distinct
 values), the gradient against mask * conv_transpose2d(dout, ones).
 """
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -195,3 +197,37 @@ def test_3x3_s2_p1_vector_path_matches_general(H, W):
         assert np.array_equal(po.to_array(out.shape), out)
         assert np.array_equal(pm.to_array((n + 1,), np.int32)[1:].reshape(x.shape), mask)
         assert np.array_equal(pd.to_array((n + 1,))[1:].reshape(x.shape), dx)
+
+
+def _random_pool_cases(n, seed):
+    """Seeded random pooling shapes: window, stride and padding combinations
+    that reach the pair, cell, 3x3-s2-p1 and general kernels, including
+    overlapping windows, odd sizes and padding up to half the window."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        KH, KW = int(r.choice([1, 2, 3, 3, 4, 5])), int(r.choice([1, 2, 3, 3, 4]))
+        s = int(r.choice([1, 2, 2, 3]))
+        p = int(r.integers(0, min(KH, KW) // 2 + 1))
+        N, C = int(r.integers(1, 4)), int(r.integers(1, 20))
+        H, W = int(r.integers(1, 30)), int(r.choice([int(r.integers(1, 30)), 4 * int(r.integers(1, 10))]))
+        if pool.out_extent(H, p, KH, s) < 1 or pool.out_extent(W, p, KW, s) < 1:
+            continue
+        out.append((f"q{len(out):02d}", N, C, H, W, KH, KW, s, p))
+    return out
+
+
+RANDOM_POOL = _random_pool_cases(24, 20261205)
+
+
+@pytest.mark.parametrize("case", RANDOM_POOL, ids=[c[0] for c in RANDOM_POOL])
+def test_parity_random_shapes(case):
+    _, N, C, H, W, KH, KW, s, p = case
+    r = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    out, mask = hip_maxpool(x, KH, KW, p, s)
+    ro, rm = pool.maxpool_fwd(x, KH, KW, p, p, s, s)
+    assert np.array_equal(out, ro) and np.array_equal(mask, rm), case
+    dout = r.standard_normal(out.shape).astype(np.float32)
+    assert np.array_equal(hip_maxpool_bwd(dout, mask, KH, KW, p, s),
+                          pool.maxpool_bwd(dout, rm, KH, KW, p, p, s, s)), case
