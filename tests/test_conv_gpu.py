@@ -128,6 +128,44 @@ def test_outputs_are_overwritten_not_accumulated():
         assert np.array_equal(pdw.to_array(w.shape), ref[1])
 
 
+@pytest.mark.parametrize("entry,C,F,K,s,p", [
+    ("seera_hip_conv2d_bwd", 64, 64, 3, 1, 1),           # the one-pass backward's shape
+    ("seera_hip_conv2d_bwd", 8, 16, 3, 2, 1),            # stride phases
+    ("seera_hip_conv2d_bwd_bias", 64, 64, 3, 1, 1),      # with db
+    ("seera_hip_conv2DTranspose_bwd", 128, 64, 4, 2, 1),  # config 5's layer
+])
+def test_empty_batch_backward_writes_zero_weight_gradient(entry, C, F, K, s, p):
+    """batch = 0: dW (and db) are sums over no images, so exactly 0, and the
+    activation pointers, which point at nothing, may be NULL. For the
+    transposed convolution W is [Cin, Cout, K, K] (upsampling.cu:322-375)."""
+    from ml_framework_amd.capi import DeviceBuffer
+    wshape = (C, F, K, K) if "Transpose" in entry else (F, C, K, K)
+    w = np.random.default_rng(C + F + K).standard_normal(wshape).astype(np.float32)
+    nbias = F if "bias" in entry else 1
+    with DeviceBuffer.from_array(w) as pw, DeviceBuffer(w.nbytes) as pdw, \
+            DeviceBuffer(nbias * 4) as pdb:
+        pdw.fill(0xFF)  # NaN everywhere until written
+        pdb.fill(0xFF)
+        extra = (pdb.ptr,) if "bias" in entry else ()
+        capi.call(entry, pw.ptr, None, None, None, pdw.ptr, *extra, 0, C, 8, 8, F, K, K, s, s, p, p)
+        assert np.array_equal(pdw.to_array(wshape), np.zeros(wshape, np.float32))
+        if extra:
+            assert np.array_equal(pdb.to_array((F,)), np.zeros(F, np.float32))
+
+
+def test_empty_batch_forward_is_a_no_op():
+    """batch = 0 forwards return success without touching memory: every
+    activation pointer NULL, the weights a real buffer."""
+    from ml_framework_amd.capi import DeviceBuffer
+    with DeviceBuffer(128 * 64 * 16 * 4) as pw:
+        pw.fill(0)
+        capi.call("seera_hip_conv2d_fwd", None, pw.ptr, None, 0, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)
+        capi.call("seera_hip_conv2d_fwd_bias_act", None, pw.ptr, None, None, None, 0, 64, 56, 56,
+                  64, 3, 3, 1, 1, 1, 1, capi.SEERA_ACT_RELU)
+        capi.call("seera_hip_conv2DTranpose_fwd", None, pw.ptr, None, 0, 128, 28, 28, 64, 4, 4,
+                  2, 2, 1, 1)
+
+
 def test_subnormal_fp16_operands_conv_identity_bit_exact():
     """A 1x1 identity convolution, and a 3x3 one with the identity on the
     centre tap (the config-4 forward and one-pass backward kernels), return
