@@ -137,3 +137,93 @@ def test_matmul_random_shape(case):
     assert_parity(da, rda, f"{case} dA")
     assert_parity(db, rdb, f"{case} dB")
     assert rel_fro(da, rda) <= STRICT and rel_fro(db, rdb) <= STRICT
+
+
+# The fused epilogues (bias + ReLU + mask in the forward stores; the ReLU
+# gradient in the dA store and db from the dB GEMM's loads of dC, or from the
+# dW pass's loads of dY) on their own seeded draws of the same ranges.
+EPI_GEMM_CASES = _gemm_cases(12, 20261205)
+EPI_CONV_CASES = _conv_cases(12, 20261206)
+
+
+def _mask_clear_agrees(mask, pre, scale):
+    """mask = (pre > 0) wherever the oracle's pre-activation is clear of 0 by
+    more than the summation-order noise (values within it may fall either way)."""
+    clear = np.abs(pre) > 1e-4 * scale
+    return np.array_equal(mask[clear], (pre[clear] > 0).astype(np.float32))
+
+
+@pytest.mark.parametrize("case", EPI_GEMM_CASES, ids=[c[0] for c in EPI_GEMM_CASES])
+def test_matmul_epilogues_random_shape(case):
+    """seera_hip_matmul_bias_act (ReLU) against the oracle's matmul + bias then
+    ReLU (tensor_ops.cpp:9-15, broadcast.cu:12-64, activations.cu:9-15), its
+    mask against the oracle's sign; seera_hip_matmul_bwd_relu_bias's dA and dB
+    against the oracle's GEMM backward times the mask, db against an fp64 sum."""
+    from ml_framework_amd.capi import DeviceBuffer
+    name, M, K, N, nb = case
+    r = np.random.default_rng(zlib.crc32(repr(case).encode()) + 1)
+    a = r.uniform(-1, 1, (nb, M, K)).astype(np.float32)
+    b = r.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = r.uniform(-1, 1, N).astype(np.float32)
+    dc = r.uniform(-1, 1, (nb, M, N)).astype(np.float32)
+    with DeviceBuffer.from_array(a) as pa, DeviceBuffer.from_array(b) as pb, \
+            DeviceBuffer.from_array(bias) as pbi, DeviceBuffer(nb * M * N * 4) as pc, \
+            DeviceBuffer(nb * M * N * 4) as pm, DeviceBuffer.from_array(dc) as pdc, \
+            DeviceBuffer(a.nbytes) as pda, DeviceBuffer(b.nbytes) as pdb, \
+            DeviceBuffer(N * 4) as pdbias:
+        capi.call("seera_hip_matmul_bias_act", pa.ptr, pb.ptr, pbi.ptr, pc.ptr, pm.ptr, M, N, K,
+                  nb, capi.SEERA_ACT_RELU)
+        got, mask = pc.to_array((nb, M, N)), pm.to_array((nb, M, N))
+        # the backward of a layer whose input a went through a ReLU: its mask
+        amask = (a > 0).astype(np.float32)
+        with DeviceBuffer.from_array(amask) as pam:
+            capi.call("seera_hip_matmul_bwd_relu_bias", pa.ptr, pb.ptr, pdc.ptr, pam.ptr, pda.ptr,
+                      pdb.ptr, pdbias.ptr, M, N, K, nb)
+        da, dbw, db = pda.to_array(a.shape), pdb.to_array(b.shape), pdbias.to_array((N,))
+    pre = S.matmul_batched(fp16r(a), fp16r(b)) + bias
+    assert_parity(got, np.where(pre > 0, pre, np.float32(0)), f"{case} fused fwd")
+    assert _mask_clear_agrees(mask, pre, np.sqrt(K))
+    rda, rdb = S.matmul_bwd(fp16r(a), fp16r(b), fp16r(dc))
+    assert_parity(da, rda * amask, f"{case} fused dA")
+    assert_parity(dbw, rdb, f"{case} dB")
+    ref = dc.astype(np.float64).sum(axis=(0, 1))
+    bound = 1e-6 * np.abs(dc).astype(np.float64).sum(axis=(0, 1)) + 1e-6
+    assert np.all(np.abs(db - ref) <= bound), f"{case} db"
+
+
+@pytest.mark.parametrize("case", EPI_CONV_CASES, ids=[c[0] for c in EPI_CONV_CASES])
+def test_conv2d_epilogues_random_shape(case):
+    """seera_hip_conv2d_fwd_bias_act (ReLU) against the oracle's conv2d_forward
+    + bias then ReLU (conv_ops.cpp:95-122, broadcast.cu:12-64,
+    activations.cu:9-15), its mask against the oracle's sign;
+    seera_hip_conv2d_bwd_bias's dX and dW against the oracle's backward, db
+    against an fp64 sum of dY over images and pixels."""
+    from ml_framework_amd.capi import DeviceBuffer
+    name, N, C, H, W, F, k, s, p = case
+    r = np.random.default_rng(zlib.crc32(repr(case).encode()) + 1)
+    x = r.standard_normal((N, C, H, W)).astype(np.float32)
+    w = _kaiming(r, (F, C, k, k), C * k * k)
+    bias = r.uniform(-0.5, 0.5, F).astype(np.float32)
+    Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    dy = r.standard_normal((N, F, Ho, Wo)).astype(np.float32)
+    ny = N * F * Ho * Wo
+    with DeviceBuffer.from_array(x) as px, DeviceBuffer.from_array(w) as pw, \
+            DeviceBuffer.from_array(bias) as pbi, DeviceBuffer(ny * 4) as py, \
+            DeviceBuffer(ny * 4) as pm, DeviceBuffer.from_array(dy) as pdy, \
+            DeviceBuffer(x.nbytes) as pdx, DeviceBuffer(w.nbytes) as pdw, \
+            DeviceBuffer(F * 4) as pdb:
+        capi.call("seera_hip_conv2d_fwd_bias_act", px.ptr, pw.ptr, pbi.ptr, py.ptr, pm.ptr, N, C,
+                  H, W, F, k, k, p, p, s, s, capi.SEERA_ACT_RELU)
+        got, mask = py.to_array(dy.shape), pm.to_array(dy.shape)
+        capi.call("seera_hip_conv2d_bwd_bias", pw.ptr, px.ptr, pdy.ptr, pdx.ptr, pdw.ptr, pdb.ptr,
+                  N, C, H, W, F, k, k, s, s, p, p)
+        dx, dw, db = pdx.to_array(x.shape), pdw.to_array(w.shape), pdb.to_array((F,))
+    pre = S.conv2d_forward(fp16r(x), fp16r(w), s, s, p, p) + bias[None, :, None, None]
+    assert_parity(got, np.where(pre > 0, pre, np.float32(0)), f"{case} fused fwd")
+    assert _mask_clear_agrees(mask, pre, np.sqrt(C * k * k))
+    rdx, rdw = S.conv2d_backward(fp16r(dy), fp16r(x), fp16r(w), s, s, p, p)
+    assert_parity(dx, rdx, f"{case} dX")
+    assert_parity(dw, rdw, f"{case} dW")
+    ref = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    bound = 1e-6 * np.abs(dy).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-6
+    assert np.all(np.abs(db - ref) <= bound), f"{case} db"
