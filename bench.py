@@ -678,7 +678,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU "
-              "(the GEMM/conv hot path is single-device; see DESIGN.md for how it would shard)",
+              "(the GEMM/conv hot path is single-device: each GPU would run its own shard of the "
+              "batch through the same kernels, with the weight gradients summed across GPUs)",
               file=sys.stderr)
         sys.exit(2)
     if args.workload and args.workload.startswith("library_"):
