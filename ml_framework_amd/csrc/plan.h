@@ -358,9 +358,12 @@ int run_plan_pair(P1 p1, const Plan& pl1, P2 p2, const Plan& pl2, hipStream_t st
                     : g == 2 ? launch_igemm_pipe_pair<32, 2>(p1, (int)nb1, p2, (int)nb2, st)
                              : launch_igemm_pipe_pair<32, 1>(p1, (int)nb1, p2, (int)nb2, st);
             else
-                e = g >= 4   ? launch_igemm_pipe_pair<64, 4>(p1, (int)nb1, p2, (int)nb2, st)
-                    : g == 2 ? launch_igemm_pipe_pair<64, 2>(p1, (int)nb1, p2, (int)nb2, st)
-                             : launch_igemm_pipe_pair<64, 1>(p1, (int)nb1, p2, (int)nb2, st);
+                // 64x64 pairs take at most two groups: with four, the 1024
+                // threads per block cost more than the shorter K ranges gain
+                // (256x784x512 backward 7.6 -> 6.9 us, 384x640x384 7.8 -> 6.4;
+                // no shape measured slower).
+                e = g >= 2 ? launch_igemm_pipe_pair<64, 2>(p1, (int)nb1, p2, (int)nb2, st)
+                           : launch_igemm_pipe_pair<64, 1>(p1, (int)nb1, p2, (int)nb2, st);
             if (e != hipSuccess) return fail_hip(e, "igemm pair launch");
             return SEERA_OK;
         }
