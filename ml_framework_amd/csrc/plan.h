@@ -24,7 +24,7 @@ struct Plan {
     Tile tile;
     int splits;
     int k_split;
-    int groups = 1;  // wave groups over the K range of a 64x64 (1, 2, 4) or 32x32 (1 .. 8) block
+    int groups = 1;  // wave groups over the K range of a 64x64 (1, 2) or 32x32 (1 .. 8) block
 };
 
 constexpr int kNumCUs = 256;
@@ -36,9 +36,11 @@ constexpr int kPipeDepth = 2;  // K slices of loads in flight in igemm_pipe_kern
 // halves of its K range (1024^3: 13.2 -> 11.1 us; four groups: 12.4 us; from
 // 512 on, the MLP's GEMMs ran no faster)
 constexpr int kGroupSplitK = 1024;
-// Largest split-K count that 64x64 tiles replace by wave groups in the block
-// (2 or 4 groups of 4 waves, no partials, no reduce launch): MLP cfg3 step
-// 67.6 -> 58.5 us; replacing up to 8 splits: 59.3 us.
+// Largest split-K count that 64x64 tiles replace by two wave groups in the
+// block (no partials, no reduce launch): MLP cfg3 step 67.6 -> 58.5 us;
+// replacing up to 8 splits: 59.3 us. Two groups, not one per split: four
+// groups (1024 threads per block) ran 3-12 % slower on every shape measured
+// (512x784x640 forward 9.9 against 8.8 us, 640x2048x640 17.2 against 15.8).
 constexpr int kMaxGroupSplits = 4;
 
 inline int tile_bm(Tile t) { return t == Tile::L ? 256 : t == Tile::M ? 128 : t == Tile::T ? 32 : 64; }
@@ -101,7 +103,7 @@ inline Plan plan_tiles(int M, int N, int K, bool big_tiles, bool allow_split,
     }
     if (allow_groups && best.tile == Tile::S) {
         if (best.splits > 1 && best.splits <= kMaxGroupSplits) {
-            best.groups = best.splits <= 2 ? 2 : 4;
+            best.groups = 2;
             best.splits = 1;
             best.k_split = std::max(K, 1);
         } else if (best.splits == 1 && K >= kGroupSplitK) {
@@ -201,9 +203,8 @@ hipError_t launch_tile(const P& p, Tile t, int splits, int groups, hipStream_t s
             case Tile::W: return launch_igemm_pipe<64, 256, 32, 1, 4, kPipeDepth>(p, splits, st);
             case Tile::M: return launch_igemm_pipe<128, 128, 32, 2, 2, kPipeDepth>(p, splits, st);
             case Tile::S:
-                // groups of 4 waves over parts of the block's K range
-                if (groups >= 4) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 4>(p, splits, st);
-                if (groups == 2) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
+                // two groups of 4 waves over the halves of the block's K range
+                if (groups >= 2) return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth, P, 2>(p, splits, st);
                 return launch_igemm_pipe<64, 64, 32, 2, 2, kPipeDepth>(p, splits, st);
             case Tile::T:
                 if (groups >= 8) return launch_igemm_pipe<32, 32, 32, 1, 1, kPipeDepth, P, 8>(p, splits, st);
@@ -358,10 +359,9 @@ int run_plan_pair(P1 p1, const Plan& pl1, P2 p2, const Plan& pl2, hipStream_t st
                     : g == 2 ? launch_igemm_pipe_pair<32, 2>(p1, (int)nb1, p2, (int)nb2, st)
                              : launch_igemm_pipe_pair<32, 1>(p1, (int)nb1, p2, (int)nb2, st);
             else
-                // 64x64 pairs take at most two groups: with four, the 1024
-                // threads per block cost more than the shorter K ranges gain
-                // (256x784x512 backward 7.6 -> 6.9 us, 384x640x384 7.8 -> 6.4;
-                // no shape measured slower).
+                // 64x64 plans take at most two groups (plan_tiles): with
+                // four, a pair ran 256x784x512 backward in 7.6 against 6.9 us
+                // and 384x640x384 in 7.8 against 6.4.
                 e = g >= 2 ? launch_igemm_pipe_pair<64, 2>(p1, (int)nb1, p2, (int)nb2, st)
                            : launch_igemm_pipe_pair<64, 1>(p1, (int)nb1, p2, (int)nb2, st);
             if (e != hipSuccess) return fail_hip(e, "igemm pair launch");

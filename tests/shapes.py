@@ -200,8 +200,8 @@ MATMUL = [
     # not from the reference's tests: 64x64 tiles over a contraction of at
     # least 1024 (two wave groups, each over half of it), with a K tail
     (512, 1057, 1000, 1), (1000, 1100, 1000, 1),
-    # few tiles: four wave groups in place of split-K, the last group's part
-    # one slice or a K tail
+    # few tiles: two wave groups in place of a three- or four-way split-K, the
+    # last group's part a K tail
     (256, 400, 256, 1), (256, 500, 256, 1),
     # 32x32 tiles (one wave per K group): 8, 4 and 2 groups, a scalar-load B,
     # a backward pair on 32x32 tiles and one that retries on 64x64 ones

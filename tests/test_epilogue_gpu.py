@@ -218,7 +218,7 @@ BWD_BIAS_SHAPES = [
     (1000, 4096, 4096, 1),  # contraction 1000 (not whole 32-slices): the other 256x256 kernel
     (1100, 512, 1024, 1),   # 64x64 tiles over a long contraction: two wave groups (dA: K 1024,
                             # dB with column sums: K 1100 with a tail)
-    (400, 256, 256, 1),     # dB with column sums over four wave groups (K 400, last part 1 slice)
+    (400, 256, 256, 1),     # dB with column sums over wave groups in place of split-K (K 400)
     (1, 1, 1, 1),
     (5, 0, 7, 1),          # K = 0: no dB rows, db from its own pass
     (0, 4, 6, 1),          # no rows: dB = 0, db = 0
