@@ -227,3 +227,46 @@ def test_conv2d_epilogues_random_shape(case):
     ref = dy.astype(np.float64).sum(axis=(0, 2, 3))
     bound = 1e-6 * np.abs(dy).astype(np.float64).sum(axis=(0, 2, 3)) + 1e-6
     assert np.all(np.abs(db - ref) <= bound), f"{case} db"
+
+
+# The specialised kernels of the configs' layer types on random geometry:
+# 3x3 stride-1 pad-1 convolutions of multiples of 64 channels (three-role
+# forward, one-pass backward, channel slices, column tiles, widened rows) and
+# 4x4 stride-2 pad-1 transposed convolutions (phase and stride-2 streaming
+# kernels), with random batch, height and width.
+def _hot_conv_cases(n, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        C = int(r.choice([64, 64, 128, 192]))
+        F = int(r.choice([64, 64, 128]))
+        N = int(r.integers(1, 5))
+        H, W = int(r.integers(1, 40)), int(r.integers(1, 130))
+        out.append((f"h{i:02d}", N, C, H, W, F, 3, 1, 1))
+    return out
+
+
+def _hot_convT_cases(n, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        Cin = int(r.choice([32, 64, 96, 128]))
+        Cout = int(r.choice([16, 32, 64]))
+        N = int(r.integers(1, 4))
+        H, W = int(r.integers(1, 24)), int(r.integers(1, 40))
+        out.append((f"u{i:02d}", N, Cin, H, W, Cout, 4, 2, 1))
+    return out
+
+
+HOT_CONV_CASES = _hot_conv_cases(12, 20261207)
+HOT_CONVT_CASES = _hot_convT_cases(10, 20261208)
+
+
+@pytest.mark.parametrize("case", HOT_CONV_CASES, ids=[c[0] for c in HOT_CONV_CASES])
+def test_conv2d_hot_path_random_geometry(case):
+    test_conv2d_random_shape(case)
+
+
+@pytest.mark.parametrize("case", HOT_CONVT_CASES, ids=[c[0] for c in HOT_CONVT_CASES])
+def test_convT_hot_path_random_geometry(case):
+    test_convT_random_shape(case)
