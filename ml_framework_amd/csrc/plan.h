@@ -33,9 +33,11 @@ constexpr int kBK = 32;      // split-K slice granularity (slice ends are predic
 constexpr int kMaxBK = 32;   // deepest K slice of any tile (tile span checks)
 constexpr int kPipeDepth = 2;  // K slices of loads in flight in igemm_pipe_kernel (4 measured no faster)
 // K per block from which a 64x64 tile runs two groups of 4 waves over the
-// halves of its K range (1024^3: 13.2 -> 11.1 us; four groups: 12.4 us; from
-// 512 on, the MLP's GEMMs ran no faster)
-constexpr int kGroupSplitK = 1024;
+// halves of its K range (1024^3: 13.2 -> 11.1 us; four groups: 12.4 us). From
+// 512 rather than 1024: 768^3 forward 10.3 -> 8.5 us (backward 19.3 -> 17.0),
+// 896^3 11.7 -> 9.5, 1000^3 13.4 -> 12.1 (its backward 25.6 -> 26.3, the one
+// case measured slower); the MLP's GEMMs, on 32x32 tiles, do not take it.
+constexpr int kGroupSplitK = 512;
 // Largest split-K count that 64x64 tiles replace by two wave groups in the
 // block (no partials, no reduce launch): MLP cfg3 step 67.6 -> 58.5 us;
 // replacing up to 8 splits: 59.3 us. Two groups, not one per split: four

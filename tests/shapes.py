@@ -198,8 +198,8 @@ MATMUL = [
     # Dense 64x784x128
     (64, 784, 128, 1),
     # not from the reference's tests: 64x64 tiles over a contraction of at
-    # least 1024 (two wave groups, each over half of it), with a K tail
-    (512, 1057, 1000, 1), (1000, 1100, 1000, 1),
+    # least 512 (two wave groups, each over half of it), with a K tail
+    (512, 1057, 1000, 1), (1000, 1100, 1000, 1), (768, 600, 768, 1), (896, 777, 640, 1),
     # few tiles: two wave groups in place of a three- or four-way split-K, the
     # last group's part a K tail
     (256, 400, 256, 1), (256, 500, 256, 1),
